@@ -1,0 +1,321 @@
+"""Benchmark of the MI355X decode hot path (one GPU).
+
+Prints ONE JSON line.  Metric: microseconds per op at batch 1
+plus achieved HBM GB/s against the 8 TB/s peak.  ``value`` is the headline
+workload, the batch-1 35B-A3B MoE decode layer (config 2, one persistent
+launch), in us/op with cold caches.  Per-op figures for the dense FFN
+(config 3), GQA attention (config 4), linear attention (config 5) and the
+other batch sizes are under ``"ops"``.
+
+Timing method (reference benchmarks/bench_utils.py:17-56, plus a cache flush):
+inputs are resident in HBM; before every timed step a 1 GiB buffer is
+rewritten so that neither the 4 MB L2s nor the 256 MB MALL hold the op's
+working set; each step is bracketed by HIP events recorded on the stream the
+kernels run on (torch's current stream); the median over K steps is reported.
+Algorithmic bytes count every weight/KV/state byte that must be read once plus
+inputs and outputs.
+
+The CPU baseline times this repository's numpy restatement of the reference's
+reference.py (``oracle/``, kind "port") on the host cores, on a bounded
+sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+REPO = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+sys.path.insert(0, str(REPO / "mega-kernel-3.6_amd"))
+
+HBM_PEAK = 8.0e12
+METRIC = "µs/op at batch 1 (MoE, dense FFN, 32K attn) + achieved HBM GB/s vs 8 TB/s peak"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# algorithmic bytes
+# ---------------------------------------------------------------------------
+
+def moe_bytes(batch, hidden, experts, inter, shared_inter, top_k, distinct, elt=2, gated=True):
+    w = experts * hidden + hidden + 3 * shared_inter * hidden + (hidden if gated else 0)
+    w += distinct * 3 * inter * hidden
+    io = batch * (2 * hidden) * elt + batch * top_k * (8 + 4)
+    return w * elt + io
+
+
+def dense_bytes(batch, hidden, inter, elt=2):
+    return (3 * hidden * inter + hidden) * elt + batch * 2 * hidden * elt
+
+
+def attn_bytes(batch, q_heads, kv_heads, head_dim, seq_len, elt=2):
+    return 2 * batch * seq_len * kv_heads * head_dim * elt + 2 * batch * q_heads * head_dim * elt
+
+
+def linear_bytes(batch, k_heads, v_heads, dk, dv, elt=2):
+    return batch * (2 * v_heads * dk * dv * 4 + 2 * k_heads * dk * elt + 2 * v_heads * dv * elt + 2 * v_heads * 4)
+
+
+# ---------------------------------------------------------------------------
+# GPU timing
+# ---------------------------------------------------------------------------
+
+class Timer:
+    def __init__(self, torch, flush_bytes=1 << 30):
+        self.torch = torch
+        self.flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device="cuda")
+
+    def run(self, fn, steps: int, warmup: int, cold: bool = True):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            if cold:
+                self.flush.add_(1.0)
+            starts[i].record()
+            fn()
+            ends[i].record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        times = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))  # us
+        return {
+            "median_us": statistics.median(times),
+            "mean_us": statistics.fmean(times),
+            "p95_us": times[min(len(times) - 1, int(math.ceil(0.95 * len(times))) - 1)],
+            "min_us": times[0],
+            "wall_s": wall,
+        }
+
+
+def with_bw(res, nbytes):
+    res = dict(res)
+    res["algorithmic_bytes"] = int(nbytes)
+    res["gbps"] = nbytes / (res["median_us"] * 1e-6) / 1e9
+    res["frac_of_8TBps"] = res["gbps"] * 1e9 / HBM_PEAK
+    return res
+
+
+# ---------------------------------------------------------------------------
+# ops
+# ---------------------------------------------------------------------------
+
+def bench_moe(mk, inputs, timer, steps, warmup, batches):
+    import torch
+
+    out = {}
+    for b in batches:
+        x, w, k = inputs.make_moe(batch=b)
+        o, idx, _ = mk.moe_decode(x, w, top_k=k)
+        distinct = int(torch.unique(idx).numel())
+        fn = lambda: mk.moe_decode(x, w, top_k=k)  # noqa: E731
+        cold = with_bw(timer.run(fn, steps, warmup, cold=True), moe_bytes(b, 2048, 256, 512, 512, k, distinct))
+        warm = timer.run(fn, steps, warmup, cold=False)
+        cold["warm_median_us"] = warm["median_us"]
+        cold["distinct_experts"] = distinct
+        out[f"moe_b{b}"] = cold
+        log(f"moe b={b}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s), {warm['median_us']:.2f} us warm")
+        if b == 1:
+            grouped = timer.run(lambda: mk.moe_decode(x, w, top_k=k, backend="grouped"), steps, warmup, cold=True)
+            out["moe_b1_torch_grouped_same_gpu"] = {"median_us": grouped["median_us"]}
+        del x, w
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_dense(mk, inputs, timer, steps, warmup, batches):
+    import torch
+
+    out = {}
+    for b in batches:
+        x, w = inputs.make_dense(batch=b)
+        fn = lambda: mk.dense_ffn_decode(x, w)  # noqa: E731
+        cold = with_bw(timer.run(fn, steps, warmup, cold=True), dense_bytes(b, 5120, 17408))
+        warm = timer.run(fn, steps, warmup, cold=False)
+        cold["warm_median_us"] = warm["median_us"]
+        out[f"dense_b{b}"] = cold
+        log(f"dense b={b}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s)")
+        if b == 1:
+            t = timer.run(lambda: mk.dense_ffn_decode(x, w, backend="torch"), steps, warmup, cold=True)
+            out["dense_b1_torch_composite_same_gpu"] = {"median_us": t["median_us"]}
+        del x, w
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
+    import torch
+
+    out = {}
+    for t in seq_lens:
+        inp = inputs.make_attention(seq_len=t)
+        fn = lambda: mk.full_attention_decode(inp)  # noqa: E731
+        cold = with_bw(timer.run(fn, steps, warmup, cold=True), attn_bytes(1, 24, 4, 256, t))
+        out[f"attn_t{t}"] = cold
+        log(f"attention T={t}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s)")
+        del inp
+        torch.cuda.empty_cache()
+    return out
+
+
+def bench_linear(mk, inputs, timer, steps, warmup, batches):
+    out = {}
+    for b in batches:
+        inp = inputs.make_gated_delta(batch=b)
+        fn = lambda: mk.linear_attention_decode(inp)  # noqa: E731
+        cold = with_bw(timer.run(fn, steps, warmup, cold=True), linear_bytes(b, 16, 32, 128, 128))
+        out[f"linear_b{b}"] = cold
+        log(f"linear b={b}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s)")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (oracle = numpy restatement of reference.py, on host cores)
+# ---------------------------------------------------------------------------
+
+def cpu_baseline_moe(inputs, budget_s: float):
+    import numpy as np
+    import torch
+
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    x, w, k = inputs.make_moe(batch=1, device="cpu")
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    args = [bits(x)] + [bits(getattr(w, f)) for f in (
+        "norm_weight", "router_weight", "expert_gate", "expert_up", "expert_down",
+        "shared_gate", "shared_up", "shared_down")]
+    sg = bits(w.shared_expert_gate)
+    oracle.moe_decode(*args, top_k=k, shared_expert_gate=sg)  # warmup
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        oracle.moe_decode(*args, top_k=k, shared_expert_gate=sg)
+        times.append((time.perf_counter() - t0) * 1e6)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": statistics.median(times),
+        "unit": "us/op",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{len(times)} calls of the numpy oracle moe_decode on config 2 at batch 1 "
+                  f"(bf16 bits upcast per call as reference.py does), median; host {cpu_model}, "
+                  f"os.cpu_count()={os.cpu_count()}",
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--ops", default="moe,dense,attn,linear")
+    ap.add_argument("--quick", action="store_true", help="batch 1 / 32K only")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
+                                   "(the multi-GPU sharding is a design note, not built)"}))
+        sys.exit(2)
+
+    import torch
+
+    import mega_kernel_qwen36 as mk
+    from tests import inputs
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    if not mk.extension_available():
+        raise RuntimeError("HIP extension not built: run mega-kernel-3.6_amd/build.py")
+    dev = torch.cuda.get_device_properties(0)
+    log(f"device {dev.name} {getattr(dev, 'gcnArchName', '')} CUs={dev.multi_processor_count}")
+
+    timer = Timer(torch)
+    ops = set(args.ops.split(","))
+    results = {}
+    t_start = time.perf_counter()
+    if "moe" in ops:
+        results.update(bench_moe(mk, inputs, timer, args.steps, args.warmup, [1] if args.quick else [1, 2, 4, 8]))
+    if "dense" in ops:
+        results.update(bench_dense(mk, inputs, timer, args.steps, args.warmup, [1] if args.quick else [1, 2, 4, 8]))
+    if "attn" in ops:
+        results.update(bench_attention(mk, inputs, timer, args.steps, args.warmup,
+                                       [32768] if args.quick else [4096, 32768, 131072]))
+    if "linear" in ops:
+        results.update(bench_linear(mk, inputs, timer, args.steps, args.warmup, [1] if args.quick else [1, 8]))
+    gpu_wall = time.perf_counter() - t_start
+
+    head = results.get("moe_b1")
+    cpu = cpu_baseline_moe(inputs, args.cpu_budget) if head is not None and args.cpu_budget > 0 else None
+    roofline = None
+    if head is not None:
+        roofline = {
+            "bound": "hbm",
+            "achieved": head["gbps"],
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": head["gbps"] * 1e9 / HBM_PEAK,
+            "traffic": None,
+            "kernel": "moe_decode_kernel",
+            "bytes_per_launch": head["algorithmic_bytes"],
+        }
+    line = {
+        "metric": METRIC,
+        "value": None if head is None else round(head["median_us"], 3),
+        "unit": "us/op",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": None if head is None else head["median_us"] / 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02^2) weights, random-init weights of the named shapes)",
+        "config": {
+            "workload": "35B-A3B MoE decode layer (config 2): hidden 2048, 256 experts top-8, "
+                        "intermediate 512, sigmoid-gated shared expert 512, batch 1, cold caches",
+            "hidden": 2048, "experts": 256, "top_k": 8, "intermediate": 512, "batch": 1,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "ops": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                for k, v in results.items()},
+        "gpu_wall_s": round(gpu_wall, 2),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,141 @@
+/*
+ * mkq.h -- C ABI of the MI355X (gfx950) decode hot path for Qwen3.6.
+ *
+ * The shared library libmkq.so exports exactly the functions declared here.
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as void*, so this header needs no HIP include), enqueues its
+ * kernels asynchronously on that stream and returns an MKQ_* status.  No
+ * entry point allocates device memory, synchronises the stream or queries
+ * the device on its call path (the CU count is read once per device and
+ * cached), so calls can be captured in a HIP graph.
+ *
+ * Tensor layouts are the reference's (row-major, contiguous):
+ *   x [batch, hidden]; router [experts, hidden];
+ *   expert_gate/up [experts, intermediate, hidden]; expert_down [experts, hidden, intermediate];
+ *   shared_gate/up [shared_intermediate, hidden]; shared_down [hidden, shared_intermediate];
+ *   q [batch, q_heads, head_dim]; k_cache/v_cache [batch, seq_len, kv_heads, head_dim];
+ *   linear q/k [batch, k_heads, key_dim]; v [batch, v_heads, value_dim];
+ *   state [batch, v_heads, key_dim, value_dim] float32.
+ * All weight/activation pointers of one call share the element type `dtype`.
+ *
+ * Workspace: entry points that need scratch take (workspace, workspace_bytes);
+ * *_workspace_bytes() gives the size.  The caller zero-fills a workspace once,
+ * before its first use; every call returns the workspace's counters to zero
+ * before its last kernel exits, so the same buffer can be reused by the next
+ * call on the same stream without clearing.  Two calls that run concurrently
+ * (different streams) must not share a workspace.
+ */
+#ifndef MKQ_H_
+#define MKQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define MKQ_OK 0
+#define MKQ_ERR_INVALID 1     /* bad shape / pointer / size: message in mkq_last_error() */
+#define MKQ_ERR_UNSUPPORTED 2 /* valid but not supported by these kernels             */
+#define MKQ_ERR_HIP 3         /* a HIP runtime call failed                            */
+
+/* element types */
+#define MKQ_DTYPE_F32 0
+#define MKQ_DTYPE_F16 1
+#define MKQ_DTYPE_BF16 2
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* mkq_last_error(void);
+
+/* ABI version (major*100 + minor). */
+int mkq_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * MoE decode.  Replaces the kernel side of
+ *   _C.moe_decode_persistent      (reference csrc/bindings.cpp:33,
+ *                                  csrc/persistent_moe_decode.cu:701-860)
+ * as called by moe_decode(backend="persistent") (mega_kernel_qwen36/ops.py:303-304).
+ * One persistent launch: RMSNorm -> router -> top-k/softmax -> routed SwiGLU
+ * experts -> shared expert (optionally scaled by sigmoid(x_norm . shared_expert_gate))
+ * -> down projection + residual.
+ * Outputs: out [batch, hidden] (dtype), indices [batch, top_k] int64 (descending
+ * logit, ties to the lower index), weights [batch, top_k] float32.
+ * shared_expert_gate may be NULL (reference behaviour: no gate).
+ * ---------------------------------------------------------------------- */
+size_t mkq_moe_decode_workspace_bytes(int batch, int hidden, int experts, int intermediate,
+                                      int shared_intermediate, int top_k);
+int mkq_moe_decode(int dtype, const void* x, const void* norm_weight, const void* router_weight,
+                   const void* expert_gate, const void* expert_up, const void* expert_down,
+                   const void* shared_gate, const void* shared_up, const void* shared_down,
+                   const void* shared_expert_gate, void* out, int64_t* indices, float* weights,
+                   int batch, int hidden, int experts, int intermediate, int shared_intermediate,
+                   int top_k, float eps, int add_residual, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dense SwiGLU FFN decode: out = down(silu(gate(rms(x))) * up(rms(x))) (+ x).
+ * No native counterpart in the reference: replaces the torch composite
+ * _dense_ffn_decode_torch (mega_kernel_qwen36/ops.py:202-218) reached from
+ * dense_ffn_decode (ops.py:323-364); semantics of reference.py:65-88.
+ * ---------------------------------------------------------------------- */
+size_t mkq_dense_ffn_decode_workspace_bytes(int batch, int hidden, int intermediate);
+int mkq_dense_ffn_decode(int dtype, const void* x, const void* norm_weight, const void* gate_weight,
+                         const void* up_weight, const void* down_weight, void* out, int batch,
+                         int hidden, int intermediate, float eps, int add_residual, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * GQA full-attention decode (one query token).  Replaces
+ *   _C.full_attention_decode      (csrc/bindings.cpp:34, csrc/attention_decode.cu:152-218)
+ * as called by full_attention_decode (ops.py:372-373).
+ * out [batch, q_heads, head_dim] (dtype) = softmax(q k^T * scale) v per q head,
+ * q head h reading kv head h / (q_heads / kv_heads).  head_dim <= 256.
+ * ---------------------------------------------------------------------- */
+size_t mkq_full_attention_decode_workspace_bytes(int batch, int q_heads, int kv_heads, int head_dim,
+                                                 int seq_len);
+int mkq_full_attention_decode(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                              void* out, int batch, int q_heads, int kv_heads, int head_dim,
+                              int seq_len, float scale, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* ------------------------------------------------------------------------
+ * Recurrent linear-attention decode, reference rule.  Replaces
+ *   _C.linear_attention_decode    (csrc/bindings.cpp:35, csrc/linear_attention_decode.cu:46-93)
+ * as called by linear_attention_decode (ops.py:378-385):
+ *   new_state = decay * state + k (x) v;   out = q^T new_state.
+ * state/new_state float32 [batch, heads, key_dim, value_dim]; new_state may
+ * equal state (in-place update).
+ * ---------------------------------------------------------------------- */
+int mkq_linear_attention_decode(int dtype, const void* q, const void* k, const void* v,
+                                const float* state, void* out, float* new_state, int batch,
+                                int heads, int key_dim, int value_dim, float decay, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Gated delta rule decode (Qwen3.6 linear attention).  No counterpart in the
+ * reference (its rule is the one above); selected by linear_attention_decode
+ * when g/beta are supplied.  Per batch row b and v head j (q/k head
+ * h = j / (v_heads / k_heads)):
+ *   S <- exp(g[b,j]) S;  S <- S + beta[b,j] k_h (x) (v_j - S^T k_h);  out_j = S^T q_h.
+ * g, beta float32 [batch, v_heads]; new_state may equal state.
+ * ---------------------------------------------------------------------- */
+int mkq_gated_delta_decode(int dtype, const void* q, const void* k, const void* v,
+                           const float* state, const float* g, const float* beta, void* out,
+                           float* new_state, int batch, int k_heads, int v_heads, int key_dim,
+                           int value_dim, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Plain GEMV used for the optional attention output projections in
+ * decode_layer: y[b, n] = sum_k w[n, k] * x[b, k] (+ residual[b, n]).
+ * No counterpart in the reference (decode_layer reshapes, ops.py:722,728).
+ * residual may be NULL.
+ * ---------------------------------------------------------------------- */
+int mkq_gemv(int dtype, const void* x, const void* w, const void* residual, void* y, int batch,
+             int in_features, int out_features, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MKQ_H_ */

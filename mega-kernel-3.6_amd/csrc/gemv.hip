@@ -1,0 +1,126 @@
+// Small-batch GEMV y[b, n] = sum_k w[n, k] x[b, k] (+ residual[b, n]) for the
+// optional attention output projections of decode_layer.  x is staged in LDS
+// as FP32; each wave streams whole weight rows with 128-bit loads.
+#include "mkq_host.h"
+
+using namespace mkq;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxNb = 4;
+constexpr int kUnroll = 4;
+
+template <typename T, int NB, bool VEC>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                        const T* __restrict__ residual, T* __restrict__ y, int kdim,
+                                                        int n, int rows_per_wg) {
+  constexpr int EPC = Epc<T>::value;
+  extern __shared__ float xs[];
+  const int kp = (kdim + EPC - 1) / EPC * EPC;
+  for (int i = threadIdx.x; i < kp; i += kThreads)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) xs[b * kp + i] = i < kdim ? to_f(x[size_t(b) * kdim + i]) : 0.f;
+  __syncthreads();
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int nch = kp / EPC;
+  const int r0 = blockIdx.x * rows_per_wg, r1 = min(n, r0 + rows_per_wg);
+  for (int r = r0 + wave; r < r1; r += kWaves) {
+    const T* row = w + size_t(r) * kdim;
+    float acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+    for (int j0 = lane; j0 < nch; j0 += kWave * kUnroll) {
+      u32x4 c[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        if (j0 + u * kWave < nch) c[u] = load_chunk_nt<T, VEC>(row, j0 + u * kWave, kdim);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int j = j0 + u * kWave;
+        if (j < nch) {
+          float f[EPC];
+          unpack(c[u], f, T{});
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) acc[b] = fmaf(f[e], xs[b * kp + j * EPC + e], acc[b]);
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float s = wave_sum(acc[b]);
+      if (lane == 0) {
+        const size_t o = size_t(b) * n + r;
+        y[o] = from_f<T>(residual ? s + to_f(residual[o]) : s);
+      }
+    }
+  }
+}
+
+template <typename T, int NB>
+int launch(const T* x, const T* w, const T* residual, T* y, int kdim, int n, hipStream_t stream) {
+  constexpr int EPC = Epc<T>::value;
+  const size_t lds = sizeof(float) * NB * size_t((kdim + EPC - 1) / EPC * EPC);
+  if (lds > size_t(max_lds_per_block()))
+    return set_error(MKQ_ERR_UNSUPPORTED, "gemv: in_features=%d too large for LDS staging", kdim);
+  const bool vec = (kdim % EPC == 0) && aligned16(w);
+  static bool attr_set = false;
+  if (!attr_set) {
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<T, NB, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block()));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<T, NB, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block()));
+    attr_set = true;
+  }
+  const int rows = 2 * kWaves;
+  const int grid = (n + rows - 1) / rows;
+  if (vec)
+    gemv_kernel<T, NB, true><<<grid, kThreads, lds, stream>>>(x, w, residual, y, kdim, n, rows);
+  else
+    gemv_kernel<T, NB, false><<<grid, kThreads, lds, stream>>>(x, w, residual, y, kdim, n, rows);
+  MKQ_LAUNCH_CHECK("gemv_kernel");
+  return MKQ_OK;
+}
+
+template <typename T>
+int gemv_typed(const void* xv, const void* wv, const void* rv, void* yv, int batch, int kdim, int n,
+               hipStream_t stream) {
+  const T* x = static_cast<const T*>(xv);
+  const T* w = static_cast<const T*>(wv);
+  const T* r = static_cast<const T*>(rv);
+  T* y = static_cast<T*>(yv);
+  for (int b0 = 0; b0 < batch; b0 += kMaxNb) {
+    const int nb = batch - b0 < kMaxNb ? batch - b0 : kMaxNb;
+    const T* xb = x + size_t(b0) * kdim;
+    const T* rb = r ? r + size_t(b0) * n : nullptr;
+    T* yb = y + size_t(b0) * n;
+    int rc;
+    switch (nb) {
+      case 1: rc = launch<T, 1>(xb, w, rb, yb, kdim, n, stream); break;
+      case 2: rc = launch<T, 2>(xb, w, rb, yb, kdim, n, stream); break;
+      case 3: rc = launch<T, 3>(xb, w, rb, yb, kdim, n, stream); break;
+      default: rc = launch<T, 4>(xb, w, rb, yb, kdim, n, stream); break;
+    }
+    if (rc != MKQ_OK) return rc;
+  }
+  return MKQ_OK;
+}
+
+}  // namespace
+
+extern "C" int mkq_gemv(int dtype, const void* x, const void* w, const void* residual, void* y, int batch,
+                        int in_features, int out_features, void* stream) {
+  clear_error();
+  MKQ_REQUIRE(batch > 0 && in_features > 0 && out_features > 0, "gemv: sizes must be positive");
+  MKQ_REQUIRE(x && w && y, "gemv: null tensor pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MKQ_DTYPE_BF16: return gemv_typed<bf16_t>(x, w, residual, y, batch, in_features, out_features, s);
+    case MKQ_DTYPE_F16: return gemv_typed<f16_t>(x, w, residual, y, batch, in_features, out_features, s);
+    case MKQ_DTYPE_F32: return gemv_typed<float>(x, w, residual, y, batch, in_features, out_features, s);
+    default: return set_error(MKQ_ERR_INVALID, "gemv: unknown dtype %d", dtype);
+  }
+}

@@ -1,0 +1,157 @@
+// Recurrent linear-attention decode for gfx950: the reference rule and the
+// gated delta rule, FP32 state.
+//
+// Reference rule (reference.py:148-166, linear_attention_decode.cu:10-42):
+//     S' = decay * S + k (x) v;            o = S'^T q
+// Gated delta rule (Qwen3.6 linear attention; v head j reads q/k head j/rep):
+//     S  = exp(g) * S;  u = v - S^T k;  S' = S + beta * k (x) u;  o = S'^T q
+//
+// Column j of S (all key rows i for one value index j) evolves independently,
+// so a workgroup owns a 64-column slice of one (batch, v-head) state: lane =
+// column (64 consecutive floats = one coalesced 256-byte row segment), the 4
+// waves split the key rows, and the two reductions over key rows (S^T k and
+// S'^T q) cross the waves through LDS.  The slice stays in VGPRs between the
+// single HBM read and the single HBM write of the state.
+#include "mkq_host.h"
+
+using namespace mkq;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxKeyDim = 256;
+constexpr int kRowsPerWave = kMaxKeyDim / kWaves;  // 64 state values per lane at most
+
+// grid: (ceil(Dv/64), Hv, B); block 256.
+template <typename T, bool GATED>
+__global__ __launch_bounds__(kThreads) void linear_attention_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* state,
+    const float* __restrict__ g, const float* __restrict__ beta, T* __restrict__ out, float* new_state, int hk,
+    int hv, int dk, int dv, float decay) {
+  __shared__ float qs[kMaxKeyDim];
+  __shared__ float ks[kMaxKeyDim];
+  __shared__ float red[kWaves][kWave];
+
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int j = blockIdx.x * kWave + lane;  // value column
+  const int vh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int rep = hv / hk;
+  const int qh = vh / rep;
+  const bool col_ok = j < dv;
+
+  for (int i = threadIdx.x; i < dk; i += kThreads) {
+    qs[i] = to_f(q[(size_t(b) * hk + qh) * dk + i]);
+    ks[i] = to_f(k[(size_t(b) * hk + qh) * dk + i]);
+  }
+  float d = decay, bt = 1.0f;
+  if constexpr (GATED) {
+    d = expf(g[size_t(b) * hv + vh]);
+    bt = beta[size_t(b) * hv + vh];
+  }
+  const float vj = col_ok ? to_f(v[(size_t(b) * hv + vh) * dv + j]) : 0.f;
+  __syncthreads();
+
+  const size_t base = (size_t(b) * hv + vh) * size_t(dk) * dv;
+  float s[kRowsPerWave];
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; ++r) {
+    const int i = wave + r * kWaves;
+    s[r] = (col_ok && i < dk) ? state[base + size_t(i) * dv + j] * d : 0.f;
+  }
+
+  float add = vj;  // reference rule: S += k (x) v
+  if constexpr (GATED) {
+    float p = 0.f;
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+      const int i = wave + r * kWaves;
+      if (i < dk) p = fmaf(s[r], ks[i], p);
+    }
+    red[wave][lane] = p;
+    __syncthreads();
+    float sk = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) sk += red[w][lane];
+    add = bt * (vj - sk);  // S += k (x) beta*(v - S^T k)
+    __syncthreads();
+  }
+
+  float o = 0.f;
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; ++r) {
+    const int i = wave + r * kWaves;
+    if (i < dk) {
+      s[r] = fmaf(ks[i], add, s[r]);
+      o = fmaf(s[r], qs[i], o);
+      if (col_ok) new_state[base + size_t(i) * dv + j] = s[r];
+    }
+  }
+  red[wave][lane] = o;
+  __syncthreads();
+  if (wave == 0 && col_ok) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t += red[w][lane];
+    out[(size_t(b) * hv + vh) * dv + j] = from_f<T>(t);
+  }
+}
+
+template <typename T, bool GATED>
+int launch(const void* q, const void* k, const void* v, const float* state, const float* g, const float* beta,
+           void* out, float* new_state, int batch, int hk, int hv, int dk, int dv, float decay, hipStream_t stream) {
+  dim3 grid((dv + kWave - 1) / kWave, hv, batch);
+  linear_attention_kernel<T, GATED><<<grid, kThreads, 0, stream>>>(
+      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), state, g, beta,
+      static_cast<T*>(out), new_state, hk, hv, dk, dv, decay);
+  MKQ_LAUNCH_CHECK("linear_attention_kernel");
+  return MKQ_OK;
+}
+
+template <bool GATED>
+int dispatch(int dtype, const void* q, const void* k, const void* v, const float* state, const float* g,
+             const float* beta, void* out, float* new_state, int batch, int hk, int hv, int dk, int dv, float decay,
+             void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MKQ_DTYPE_BF16:
+      return launch<bf16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, s);
+    case MKQ_DTYPE_F16:
+      return launch<f16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, s);
+    case MKQ_DTYPE_F32:
+      return launch<float, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, s);
+    default:
+      return set_error(MKQ_ERR_INVALID, "linear attention: unknown dtype %d", dtype);
+  }
+}
+
+}  // namespace
+
+extern "C" int mkq_linear_attention_decode(int dtype, const void* q, const void* k, const void* v, const float* state,
+                                           void* out, float* new_state, int batch, int heads, int key_dim,
+                                           int value_dim, float decay, void* stream) {
+  clear_error();
+  MKQ_REQUIRE(batch > 0 && heads > 0 && key_dim > 0 && value_dim > 0, "linear_attention_decode: sizes must be positive");
+  MKQ_REQUIRE(q && k && v && state && out && new_state, "linear_attention_decode: null tensor pointer");
+  if (key_dim > kMaxKeyDim)
+    return set_error(MKQ_ERR_UNSUPPORTED, "linear_attention_decode: key_dim %d > %d", key_dim, kMaxKeyDim);
+  MKQ_REQUIRE(batch <= 65535 && heads <= 65535, "linear_attention_decode: batch/heads too large");
+  return dispatch<false>(dtype, q, k, v, state, nullptr, nullptr, out, new_state, batch, heads, heads, key_dim,
+                         value_dim, decay, stream);
+}
+
+extern "C" int mkq_gated_delta_decode(int dtype, const void* q, const void* k, const void* v, const float* state,
+                                      const float* g, const float* beta, void* out, float* new_state, int batch,
+                                      int k_heads, int v_heads, int key_dim, int value_dim, void* stream) {
+  clear_error();
+  MKQ_REQUIRE(batch > 0 && k_heads > 0 && v_heads > 0 && key_dim > 0 && value_dim > 0,
+              "gated_delta_decode: sizes must be positive");
+  MKQ_REQUIRE(v_heads % k_heads == 0, "gated_delta_decode: v_heads must be a multiple of k_heads");
+  MKQ_REQUIRE(q && k && v && state && g && beta && out && new_state, "gated_delta_decode: null tensor pointer");
+  if (key_dim > kMaxKeyDim)
+    return set_error(MKQ_ERR_UNSUPPORTED, "gated_delta_decode: key_dim %d > %d", key_dim, kMaxKeyDim);
+  MKQ_REQUIRE(batch <= 65535 && v_heads <= 65535, "gated_delta_decode: batch/heads too large");
+  return dispatch<true>(dtype, q, k, v, state, g, beta, out, new_state, batch, k_heads, v_heads, key_dim, value_dim,
+                        1.0f, stream);
+}

@@ -1,0 +1,376 @@
+"""Decode-path operator API for Qwen3.6 on MI355X (gfx950).
+
+Drop-in for the reference's ``mega_kernel_qwen36/ops.py`` decode surface:
+``moe_decode``, ``dense_ffn_decode``, ``full_attention_decode``,
+``linear_attention_decode`` and ``decode_layer`` keep their signatures,
+dataclasses and ``ValueError`` messages.  The default backends run the
+hand-written HIP kernels of ``libmkq.so`` through the ``_C`` extension.
+
+Differences from the reference, all deliberate:
+
+* There is no silent fallback.  When ``_C`` is missing or a tensor is not on a
+  GPU, the HIP backends raise ``RuntimeError``.  The reference instead drops to
+  its CPU ``reference.py`` (ops.py:29-32,149-150,307).
+* ``backend="reference"`` names the CPU oracle.  This build keeps the oracle
+  outside the product (it is test infrastructure), so asking for it raises.
+* ``backend="auto"`` goes to the HIP kernels for MoE and the dense FFN.  The
+  reference sends ``auto`` to the grouped torch composite (ops.py:299-300,
+  340-341).  ``"grouped"`` (MoE) and ``"torch"`` (dense) are still available
+  as explicitly chosen torch composites, and ``"triton"`` maps to HIP.
+* Optional extensions used by the Qwen3.6 shapes (reference has no code for
+  them): ``GatedMoeWeights.shared_expert_gate`` (sigmoid-gated shared expert),
+  ``LinearAttentionInputs.g/beta`` (gated delta rule) and ``out_proj`` on both
+  attention input dataclasses (projection onto the hidden size inside
+  ``decode_layer``).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from .config import qwen36_layer_type
+
+try:
+    from . import _C  # HIP kernels (libmkq.so) behind a thin torch binding
+    _C_IMPORT_ERROR: Optional[BaseException] = None
+except Exception as exc:  # pragma: no cover - exercised when the extension is not built
+    _C = None
+    _C_IMPORT_ERROR = exc
+
+
+# ---------------------------------------------------------------------------
+# dataclasses (reference ops.py:38-75,129-136)
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class MoeWeights:
+    norm_weight: torch.Tensor
+    router_weight: torch.Tensor
+    expert_gate: torch.Tensor
+    expert_up: torch.Tensor
+    expert_down: torch.Tensor
+    shared_gate: torch.Tensor
+    shared_up: torch.Tensor
+    shared_down: torch.Tensor
+
+
+@dataclass(frozen=True)
+class GatedMoeWeights(MoeWeights):
+    """MoE weights whose shared expert is scaled by ``sigmoid(x_norm . shared_expert_gate)``.
+
+    ``shared_expert_gate`` is ``[hidden]`` or ``[1, hidden]``; the gate reads the
+    post-RMSNorm activation (as Qwen3-Next/Qwen3.6's sparse MoE block does).
+    """
+
+    shared_expert_gate: torch.Tensor = None  # type: ignore[assignment]
+
+
+@dataclass(frozen=True)
+class DenseFfnWeights:
+    norm_weight: torch.Tensor
+    gate_weight: torch.Tensor
+    up_weight: torch.Tensor
+    down_weight: torch.Tensor
+
+
+@dataclass(frozen=True)
+class FullAttentionInputs:
+    q: torch.Tensor
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    cos: Optional[torch.Tensor] = None
+    sin: Optional[torch.Tensor] = None
+    rotary_dim: int = 64
+    scale: Optional[float] = None
+    out_proj: Optional[torch.Tensor] = None  # [hidden, q_heads*head_dim], used by decode_layer
+
+
+@dataclass(frozen=True)
+class LinearAttentionInputs:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    state: torch.Tensor
+    decay: float = 1.0
+    g: Optional[torch.Tensor] = None      # [batch, v_heads] f32: selects the gated delta rule
+    beta: Optional[torch.Tensor] = None   # [batch, v_heads] f32
+    out_proj: Optional[torch.Tensor] = None  # [hidden, v_heads*value_dim], used by decode_layer
+
+
+@dataclass(frozen=True)
+class DecodeLayerResult:
+    hidden: torch.Tensor
+    router_indices: Optional[torch.Tensor] = None
+    router_weights: Optional[torch.Tensor] = None
+    attention_output: Optional[torch.Tensor] = None
+    linear_output: Optional[torch.Tensor] = None
+    linear_state: Optional[torch.Tensor] = None
+
+
+# ---------------------------------------------------------------------------
+# dispatch predicates (reference ops.py:145-158)
+# ---------------------------------------------------------------------------
+
+def extension_available() -> bool:
+    return _C is not None
+
+
+def _use_extension(*tensors: torch.Tensor) -> bool:
+    return _C is not None and all(t.is_cuda for t in tensors)
+
+
+def _require_extension(op: str, *tensors: torch.Tensor) -> None:
+    if _C is None:
+        raise RuntimeError(
+            f"{op}: the HIP extension mega_kernel_qwen36._C is not loaded "
+            f"({_C_IMPORT_ERROR!r}); build it with mega-kernel-3.6_amd/build.py"
+        )
+    if not all(t.is_cuda for t in tensors):
+        raise RuntimeError(f"{op}: the HIP kernels need every tensor on a GPU (got a CPU tensor)")
+
+
+def _matmul_dtype(x: torch.Tensor) -> torch.dtype:
+    return x.dtype if (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16)) else torch.float32
+
+
+def _no_reference(op: str) -> RuntimeError:
+    return RuntimeError(
+        f"{op}: backend='reference' is the CPU oracle, which this build keeps as test infrastructure "
+        "(oracle/); use the HIP backend ('auto')"
+    )
+
+
+def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# torch composites (explicitly chosen backends only)
+# ---------------------------------------------------------------------------
+
+def _moe_decode_grouped_torch(x, w: MoeWeights, *, eps, top_k, add_residual):
+    """Grouped-GEMM torch composite of the MoE (the reference's "grouped" backend, ops.py:161-199)."""
+    x_norm = _rms_norm(x, w.norm_weight, eps).float()
+    topk_logits, topk_idx = torch.topk(x_norm @ w.router_weight.float().t(), k=top_k, dim=-1)
+    topk_w = torch.softmax(topk_logits, dim=-1)
+    batch, hidden = x.shape
+    mm = _matmul_dtype(x)
+    sel = topk_idx.reshape(-1)
+    xs = x_norm.to(mm).repeat_interleave(top_k, dim=0).unsqueeze(-1).contiguous()  # [B*k, H, 1]
+    gate = torch.bmm(w.expert_gate.index_select(0, sel), xs).squeeze(-1).float()
+    up = torch.bmm(w.expert_up.index_select(0, sel), xs).squeeze(-1).float()
+    act = F.silu(gate) * up * topk_w.reshape(-1, 1)
+    routed = torch.bmm(w.expert_down.index_select(0, sel), act.to(mm).unsqueeze(-1).contiguous())
+    routed = routed.squeeze(-1).float().view(batch, top_k, hidden).sum(dim=1)
+    xm = x_norm.to(mm)
+    shared_act = F.silu(F.linear(xm, w.shared_gate).float()) * F.linear(xm, w.shared_up).float()
+    shared = F.linear(shared_act.to(mm), w.shared_down).float()
+    sg = getattr(w, "shared_expert_gate", None)
+    if sg is not None:
+        shared = shared * torch.sigmoid(x_norm @ sg.float().reshape(-1, 1))
+    out = routed + shared
+    if add_residual:
+        out = out + x.float()
+    return out.to(x.dtype), topk_idx, topk_w
+
+
+def _dense_ffn_decode_torch(x, w: DenseFfnWeights, *, eps, add_residual):
+    """torch composite of the dense FFN (the reference's "torch" backend, ops.py:202-218)."""
+    mm = _matmul_dtype(x)
+    xm = _rms_norm(x, w.norm_weight, eps).to(mm)
+    act = F.silu(F.linear(xm, w.gate_weight).float()) * F.linear(xm, w.up_weight).float()
+    out = F.linear(act.to(mm), w.down_weight).float()
+    if add_residual:
+        out = out + x.float()
+    return out.to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# public decode ops
+# ---------------------------------------------------------------------------
+
+def _moe_tensors(x, weights: MoeWeights):
+    return (
+        x,
+        weights.norm_weight,
+        weights.router_weight,
+        weights.expert_gate,
+        weights.expert_up,
+        weights.expert_down,
+        weights.shared_gate,
+        weights.shared_up,
+        weights.shared_down,
+    )
+
+
+def moe_decode(
+    x: torch.Tensor,
+    weights: MoeWeights,
+    *,
+    eps: float = 1e-6,
+    top_k: int = 8,
+    add_residual: bool = True,
+    backend: str = "auto",
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused MoE decode step.  Returns ``(out [B,H] x.dtype, indices [B,k] int64, weights [B,k] f32)``.
+
+    ``auto``/``persistent``: one persistent HIP launch (RMSNorm, router, top-k
+    softmax, routed SwiGLU experts, shared expert, down projection, residual).
+    """
+    if backend not in {"auto", "persistent", "grouped", "reference"}:
+        raise ValueError("backend must be one of: auto, persistent, grouped, reference")
+    tensors = _moe_tensors(x, weights)
+    if backend == "grouped":
+        return _moe_decode_grouped_torch(x, weights, eps=eps, top_k=top_k, add_residual=add_residual)
+    if backend == "reference":
+        raise _no_reference("moe_decode")
+    _require_extension("moe_decode", *tensors)
+    sg = getattr(weights, "shared_expert_gate", None)
+    if sg is not None:
+        return _C.moe_decode_persistent_gated(*tensors, sg, float(eps), int(top_k), bool(add_residual))
+    return _C.moe_decode_persistent(*tensors, float(eps), int(top_k), bool(add_residual))
+
+
+def dense_ffn_decode(
+    x: torch.Tensor,
+    weights: DenseFfnWeights,
+    *,
+    eps: float = 1e-6,
+    add_residual: bool = True,
+    backend: str = "auto",
+) -> torch.Tensor:
+    """Fused RMSNorm + SwiGLU FFN decode step (HIP).  ``x [B,H]`` -> ``[B,H]``."""
+    tensors = (x, weights.norm_weight, weights.gate_weight, weights.up_weight, weights.down_weight)
+    if backend not in {"auto", "torch", "triton", "reference"}:
+        raise ValueError("backend must be one of: auto, torch, triton, reference")
+    if backend == "torch":
+        return _dense_ffn_decode_torch(x, weights, eps=eps, add_residual=add_residual)
+    if backend == "reference":
+        raise _no_reference("dense_ffn_decode")
+    _require_extension("dense_ffn_decode", *tensors)
+    return _C.dense_ffn_decode(*tensors, float(eps), bool(add_residual))
+
+
+def apply_partial_rope(q, k, cos, sin, rotary_dim: int):
+    """Rotate-half RoPE on the first ``rotary_dim`` dims of q and k (reference.py:91-114)."""
+    if cos is None or sin is None or rotary_dim <= 0:
+        return q, k
+    half = rotary_dim // 2
+    cos = cos.to(device=q.device, dtype=torch.float32)
+    sin = sin.to(device=q.device, dtype=torch.float32)
+
+    def rotate(t):
+        tr = t[..., :rotary_dim].float()
+        rh = torch.cat((-tr[..., half:], tr[..., :half]), dim=-1)
+        c, s = cos, sin
+        while c.ndim < tr.ndim:
+            c, s = c.unsqueeze(0), s.unsqueeze(0)
+        return torch.cat(((tr * c + rh * s).to(t.dtype), t[..., rotary_dim:]), dim=-1)
+
+    return rotate(q), rotate(k)
+
+
+def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:
+    """One-token GQA attention over a contiguous KV cache (split-K flash-decode, HIP)."""
+    q, k_cache = apply_partial_rope(inputs.q, inputs.k_cache, inputs.cos, inputs.sin, inputs.rotary_dim)
+    scale = inputs.scale
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    if q.shape[1] % k_cache.shape[2] != 0:
+        raise ValueError("query_heads must be divisible by kv_heads")
+    _require_extension("full_attention_decode", q, k_cache, inputs.v_cache)
+    return _C.full_attention_decode(q.contiguous(), k_cache.contiguous(), inputs.v_cache.contiguous(), float(scale))
+
+
+def linear_attention_decode(inputs: LinearAttentionInputs) -> tuple[torch.Tensor, torch.Tensor]:
+    """One recurrent step.  Returns ``(out, new_state)``; the input state is not modified.
+
+    Without ``g``/``beta``: the reference rule ``S' = decay*S + k v^T``, ``o = q^T S'``.
+    With them: the gated delta rule (v head j reads q/k head ``j // (Hv // Hk)``).
+    """
+    if (inputs.g is None) != (inputs.beta is None):
+        raise ValueError("g and beta must be given together")
+    tensors = (inputs.q, inputs.k, inputs.v, inputs.state)
+    if inputs.g is not None:
+        _require_extension("linear_attention_decode", *tensors, inputs.g, inputs.beta)
+        return _C.gated_delta_decode(
+            inputs.q.contiguous(),
+            inputs.k.contiguous(),
+            inputs.v.contiguous(),
+            inputs.state.contiguous(),
+            inputs.g.float().contiguous(),
+            inputs.beta.float().contiguous(),
+        )
+    _require_extension("linear_attention_decode", *tensors)
+    return _C.linear_attention_decode(
+        inputs.q.contiguous(),
+        inputs.k.contiguous(),
+        inputs.v.contiguous(),
+        inputs.state.contiguous(),
+        float(inputs.decay),
+    )
+
+
+def _project(out: torch.Tensor, out_proj: Optional[torch.Tensor], hidden: torch.Tensor) -> torch.Tensor:
+    if out_proj is None:
+        return out.reshape_as(hidden)
+    _require_extension("decode_layer out_proj", out, out_proj)
+    return _C.gemv(out.reshape(out.shape[0], -1).contiguous(), out_proj.contiguous(), None)
+
+
+def decode_layer(
+    layer_idx: int,
+    hidden: torch.Tensor,
+    moe: Optional[MoeWeights] = None,
+    *,
+    dense_ffn: Optional[DenseFfnWeights] = None,
+    full_attention: Optional[FullAttentionInputs] = None,
+    linear_attention: Optional[LinearAttentionInputs] = None,
+    layer_type: Optional[str] = None,
+    eps: float = 1e-6,
+    top_k: int = 8,
+) -> DecodeLayerResult:
+    """One decoder layer step (reference ops.py:701-748): attention or linear
+    attention plus residual, then dense FFN or MoE with the residual inside."""
+    kind = layer_type or qwen36_layer_type(layer_idx)
+    attention_output = None
+    linear_output = None
+    linear_state = None
+    residual = hidden
+
+    if kind == "full_attention":
+        if full_attention is None:
+            raise ValueError("full_attention inputs are required for full_attention layers")
+        attention_output = _project(full_attention_decode(full_attention), full_attention.out_proj, hidden)
+        residual = residual + attention_output
+    elif kind == "linear_attention":
+        if linear_attention is None:
+            raise ValueError("linear_attention inputs are required for linear_attention layers")
+        linear_output, linear_state = linear_attention_decode(linear_attention)
+        linear_output = _project(linear_output, linear_attention.out_proj, hidden)
+        residual = residual + linear_output
+    else:
+        raise ValueError(f"unsupported layer_type: {kind}")
+
+    if dense_ffn is not None:
+        out = dense_ffn_decode(residual, dense_ffn, eps=eps, add_residual=True)
+        router_indices = None
+        router_weights = None
+    else:
+        if moe is None:
+            raise ValueError("either moe or dense_ffn weights are required")
+        out, router_indices, router_weights = moe_decode(residual, moe, eps=eps, top_k=top_k, add_residual=True)
+    return DecodeLayerResult(
+        hidden=out,
+        router_indices=router_indices,
+        router_weights=router_weights,
+        attention_output=attention_output,
+        linear_output=linear_output,
+        linear_state=linear_state,
+    )

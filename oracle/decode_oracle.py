@@ -1,0 +1,411 @@
+"""CPU oracle for the single-token decode hot path (numpy, FP32).
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the shipped package imports this
+module: only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
+leg of ``bench.py`` may use it, and only as the checker (or, for the CPU
+baseline, as the thing timed on the host cores).  The HIP path never routes
+through it.
+
+Each function restates one function of the reference's
+``mega_kernel_qwen36/reference.py`` from its text, keeping its op structure
+(FP32 upcast of every weight on every call, the Python loop over
+batch x top-k in MoE, the per-query-head loop in attention) so that timing it
+is a fair "reference CPU path" figure.  Inputs are numpy arrays:
+
+* ``float32`` arrays are used as is;
+* ``uint16`` arrays are bfloat16 bit patterns and are upcast on every call,
+  as ``tensor.float()`` does in the reference.
+
+Two behaviours are added where the task's shapes need them and the reference
+has no code for them; both are documented at their functions:
+
+* the sigmoid-gated shared expert (``shared_expert_gate``), applied to the
+  post-RMSNorm activation, as the HF ``Qwen3NextSparseMoeBlock`` does;
+* the gated delta rule for linear attention (``gated_delta_decode``), with
+  v-head ``j`` reading q/k head ``j // (Hv // Hk)``.
+
+Pinning (what checks each function independently of its own text) is listed
+in ``PINNING`` at the bottom of this file and exercised by
+``tests/test_oracle.py``: closed forms, invariants, torch library routines
+(``torch.topk``, ``F.scaled_dot_product_attention(enable_gqa=True)``,
+``F.rms_norm``) and committed golden vectors written by an independent
+float64 torch composition (``tests/golden/make_golden.py``).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+
+__all__ = [
+    "as_f32",
+    "bf16_bits",
+    "bf16_round",
+    "rms_norm",
+    "silu",
+    "topk_desc",
+    "softmax",
+    "moe_decode",
+    "dense_ffn_decode",
+    "apply_partial_rope",
+    "full_attention_decode",
+    "linear_attention_decode",
+    "gated_delta_decode",
+    "decode_layer",
+    "PINNING",
+]
+
+
+# ---------------------------------------------------------------------------
+# dtype helpers
+# ---------------------------------------------------------------------------
+
+def as_f32(a) -> np.ndarray:
+    """Upcast to float32.  ``uint16`` input is taken as bfloat16 bits."""
+    a = np.asarray(a)
+    if a.dtype == np.uint16:
+        return (a.astype(np.uint32) << np.uint32(16)).view(np.float32)
+    return a.astype(np.float32, copy=False)
+
+
+def bf16_bits(a) -> np.ndarray:
+    """Round float32 to bfloat16 (nearest-even) and return the bit patterns."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    rounding = np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))
+    out = ((u + rounding) >> np.uint64(16)).astype(np.uint16)
+    nan = np.isnan(a)
+    if nan.any():
+        out[nan] = np.uint16(0x7FC0)
+    return out
+
+
+def bf16_round(a) -> np.ndarray:
+    """float32 -> bfloat16 -> float32 (what ``.to(torch.bfloat16).float()`` does)."""
+    return as_f32(bf16_bits(a))
+
+
+# ---------------------------------------------------------------------------
+# elementwise / small pieces
+# ---------------------------------------------------------------------------
+
+def rms_norm(x, weight, eps: float = 1e-6) -> np.ndarray:
+    """``x * rsqrt(mean(x^2) + eps) * weight`` in FP32 (reference.py:10-13).
+
+    The reference ends with ``.to(x.dtype)``; for the FP32 inputs the oracle is
+    run on that cast is the identity, so the result stays FP32 here.
+    """
+    xf = as_f32(x)
+    var = np.mean(xf * xf, axis=-1, keepdims=True, dtype=np.float32)
+    inv = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    return (xf * inv * as_f32(weight)).astype(np.float32)
+
+
+def silu(a: np.ndarray) -> np.ndarray:
+    a = a.astype(np.float32, copy=False)
+    return (a / (np.float32(1.0) + np.exp(-a))).astype(np.float32)
+
+
+def sigmoid(a):
+    a = np.asarray(a, dtype=np.float32)
+    return (np.float32(1.0) / (np.float32(1.0) + np.exp(-a))).astype(np.float32)
+
+
+def topk_desc(logits: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """Top-k along the last axis, descending, ties to the lower index.
+
+    ``torch.topk(..., sorted=True)`` order (reference.py:44).  The tie rule is
+    the one the reference CUDA kernel implements with a strict ``>`` while
+    scanning indices upward (persistent_moe_decode.cu:333).
+    """
+    order = np.argsort(-logits, axis=-1, kind="stable")[..., :k]
+    vals = np.take_along_axis(logits, order, axis=-1)
+    return vals.astype(np.float32), order.astype(np.int64)
+
+
+def softmax(a: np.ndarray, axis: int = -1) -> np.ndarray:
+    a = a.astype(np.float32, copy=False)
+    m = np.max(a, axis=axis, keepdims=True)
+    e = np.exp(a - m)
+    return (e / np.sum(e, axis=axis, keepdims=True)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# MoE  (reference.py:16-62)
+# ---------------------------------------------------------------------------
+
+def moe_decode(
+    x,
+    norm_weight,
+    router_weight,
+    expert_gate,
+    expert_up,
+    expert_down,
+    shared_gate,
+    shared_up,
+    shared_down,
+    *,
+    eps: float = 1e-6,
+    top_k: int = 8,
+    add_residual: bool = True,
+    shared_expert_gate=None,
+) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Restates ``moe_decode_reference`` (reference.py:16-62).
+
+    x [B,H]; router [E,H]; expert_gate/up [E,I,H]; expert_down [E,H,I];
+    shared_gate/up [Is,H]; shared_down [H,Is].
+
+    ``shared_expert_gate`` ([H] or [1,H]) is the extension for the Qwen3.6
+    shape: the shared expert's output is scaled by ``sigmoid(x_norm . w_sg)``
+    per row, with ``x_norm`` the post-RMSNorm activation.  ``None`` keeps the
+    reference behaviour exactly.
+
+    Returns (out [B,H] f32, indices [B,k] int64, weights [B,k] f32).
+    """
+    x_f = as_f32(x)
+    x_norm = rms_norm(x_f, norm_weight, eps)                        # :42
+    logits = (x_norm @ as_f32(router_weight).T).astype(np.float32)  # :43
+    topk_logits, topk_idx = topk_desc(logits, top_k)                 # :44
+    topk_w = softmax(topk_logits, axis=-1)                           # :45
+
+    batch, hidden = x_f.shape
+    out = np.zeros((batch, hidden), dtype=np.float32)                # :48
+    for b in range(batch):                                           # :50-56
+        for slot in range(top_k):
+            e = int(topk_idx[b, slot])
+            w = topk_w[b, slot]
+            gate = silu(as_f32(expert_gate[e]) @ x_norm[b])
+            up = as_f32(expert_up[e]) @ x_norm[b]
+            out[b] += w * (as_f32(expert_down[e]) @ (gate * up))
+
+    shared = silu(x_norm @ as_f32(shared_gate).T) * (x_norm @ as_f32(shared_up).T)  # :58
+    shared_out = (shared @ as_f32(shared_down).T).astype(np.float32)                 # :59
+    if shared_expert_gate is not None:
+        wsg = as_f32(shared_expert_gate).reshape(-1)
+        factor = sigmoid(x_norm @ wsg)                                # [B]
+        shared_out = shared_out * factor[:, None]
+    out += shared_out
+    if add_residual:                                                  # :60-61
+        out += x_f
+    return out.astype(np.float32), topk_idx, topk_w
+
+
+# ---------------------------------------------------------------------------
+# Dense SwiGLU FFN  (reference.py:65-88)
+# ---------------------------------------------------------------------------
+
+def dense_ffn_decode(x, norm_weight, gate_weight, up_weight, down_weight, *, eps=1e-6, add_residual=True):
+    """Restates ``dense_ffn_decode_reference`` (reference.py:65-88)."""
+    x_f = as_f32(x)
+    x_norm = rms_norm(x_f, norm_weight, eps)                                        # :83
+    act = silu(x_norm @ as_f32(gate_weight).T) * (x_norm @ as_f32(up_weight).T)      # :84
+    out = (act @ as_f32(down_weight).T).astype(np.float32)                          # :85
+    if add_residual:
+        out += x_f                                                                  # :86-87
+    return out.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Partial RoPE  (reference.py:91-114)
+# ---------------------------------------------------------------------------
+
+def apply_partial_rope(q, k, cos, sin, rotary_dim: int):
+    """Rotate-half RoPE on the first ``rotary_dim`` dims (reference.py:91-114)."""
+    if cos is None or sin is None or rotary_dim <= 0:
+        return as_f32(q), as_f32(k)
+    q = as_f32(q)
+    k = as_f32(k)
+    cos = as_f32(cos)
+    sin = as_f32(sin)
+    half = rotary_dim // 2
+
+    def rot_half(t):
+        return np.concatenate((-t[..., half:rotary_dim], t[..., :half]), axis=-1)
+
+    q_rot, q_pass = q[..., :rotary_dim], q[..., rotary_dim:]
+    k_rot, k_pass = k[..., :rotary_dim], k[..., rotary_dim:]
+    while cos.ndim < q_rot.ndim:
+        cos = cos[None]
+        sin = sin[None]
+    q_out = q_rot * cos + rot_half(q_rot) * sin
+    kc, ks = cos, sin
+    while kc.ndim < k_rot.ndim:
+        kc = kc[None]
+        ks = ks[None]
+    k_out = k_rot * kc + rot_half(k_rot) * ks
+    return (np.concatenate((q_out, q_pass), axis=-1).astype(np.float32),
+            np.concatenate((k_out, k_pass), axis=-1).astype(np.float32))
+
+
+# ---------------------------------------------------------------------------
+# GQA attention decode  (reference.py:117-145)
+# ---------------------------------------------------------------------------
+
+def full_attention_decode(q, k_cache, v_cache, *, scale: Optional[float] = None) -> np.ndarray:
+    """Restates ``full_attention_decode_reference`` (reference.py:117-145).
+
+    q [B,Hq,D]; k_cache/v_cache [B,T,Hkv,D]; q-head ``qh`` reads kv head
+    ``qh // (Hq // Hkv)``.  Returns [B,Hq,D] f32.
+    """
+    q = np.asarray(q)
+    batch, query_heads, head_dim = q.shape
+    kv_heads = k_cache.shape[2]
+    if query_heads % kv_heads != 0:
+        raise ValueError("query_heads must be divisible by kv_heads")   # :133-134
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    group = query_heads // kv_heads
+    outs = []
+    for qh in range(query_heads):                                         # :140-144
+        kvh = qh // group
+        qf = as_f32(q[:, qh])                                             # [B,D]
+        kf = as_f32(k_cache[:, :, kvh])                                   # [B,T,D]
+        vf = as_f32(v_cache[:, :, kvh])
+        scores = np.einsum("bd,btd->bt", qf, kf).astype(np.float32) * np.float32(scale)
+        probs = softmax(scores, axis=-1)
+        outs.append(np.einsum("bt,btd->bd", probs, vf).astype(np.float32))
+    return np.stack(outs, axis=1).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Linear attention  (reference.py:148-166) and the gated delta rule
+# ---------------------------------------------------------------------------
+
+def linear_attention_decode(q, k, v, state, *, decay: float = 1.0):
+    """Restates ``linear_attention_decode_reference`` (reference.py:148-166).
+
+    ``S' = decay * S + k (x) v``;  ``o = q^T S'``.
+    q/k [B,H,Dk]; v [B,H,Dv]; state [B,H,Dk,Dv].  Returns (o f32, S' f32).
+    """
+    new_state = as_f32(state) * np.float32(decay) + np.einsum("bhd,bhv->bhdv", as_f32(k), as_f32(v))
+    new_state = new_state.astype(np.float32)
+    out = np.einsum("bhd,bhdv->bhv", as_f32(q), new_state).astype(np.float32)
+    return out, new_state
+
+
+def gated_delta_decode(q, k, v, state, g, beta):
+    """Gated delta rule, one decode step (the task's config-5 formula).
+
+    Per batch row b and v-head j (q/k head ``h = j // (Hv // Hk)``)::
+
+        S  <- exp(g[b,j]) * S
+        u  <- v[b,j] - S^T k[b,h]
+        S  <- S + beta[b,j] * k[b,h] (x) u
+        o  <- S^T q[b,h]
+
+    No 1/sqrt(Dk) scale is applied to q (a caller folds it into q).
+    q/k [B,Hk,Dk]; v [B,Hv,Dv]; state [B,Hv,Dk,Dv] f32; g/beta [B,Hv] f32.
+    Returns (o [B,Hv,Dv] f32, new_state f32).
+    """
+    qf, kf, vf = as_f32(q), as_f32(k), as_f32(v)
+    s = as_f32(state).copy()
+    g = as_f32(g)
+    beta = as_f32(beta)
+    batch, hk, dk = qf.shape
+    hv = vf.shape[1]
+    if hv % hk != 0:
+        raise ValueError("value heads must be a multiple of key heads")
+    rep = hv // hk
+    out = np.empty((batch, hv, vf.shape[2]), dtype=np.float32)
+    for b in range(batch):
+        for j in range(hv):
+            h = j // rep
+            sj = s[b, j] * np.float32(np.exp(g[b, j]))                      # [Dk,Dv]
+            u = vf[b, j] - kf[b, h] @ sj                                     # [Dv]
+            sj = sj + np.float32(beta[b, j]) * np.outer(kf[b, h], u).astype(np.float32)
+            s[b, j] = sj
+            out[b, j] = qf[b, h] @ sj
+    return out, s.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# decode_layer composition  (ops.py:701-748)
+# ---------------------------------------------------------------------------
+
+def decode_layer(
+    hidden,
+    *,
+    kind: str,
+    moe: Optional[dict] = None,
+    dense_ffn: Optional[dict] = None,
+    full_attention: Optional[dict] = None,
+    linear_attention: Optional[dict] = None,
+    eps: float = 1e-6,
+    top_k: int = 8,
+    round_to_bf16: bool = True,
+):
+    """Restates ``decode_layer`` (ops.py:701-748) over the oracle's ops.
+
+    The dicts carry the same fields as the API's dataclasses.  An ``out_proj``
+    entry ([H, heads*dim]) projects the attention output onto the hidden size
+    before the residual add; without it the output is reshaped, as in the
+    reference (ops.py:722,728).  With ``round_to_bf16`` each op's output is
+    rounded to bfloat16 before it feeds the next op, as it is on the bf16
+    device path.
+    """
+    h = as_f32(hidden)
+    rnd = bf16_round if round_to_bf16 else (lambda a: a)
+    res = {"attention_output": None, "linear_output": None, "linear_state": None,
+           "router_indices": None, "router_weights": None}
+    if kind == "full_attention":
+        if full_attention is None:
+            raise ValueError("full_attention inputs are required for full_attention layers")
+        fa = full_attention
+        q, kc = apply_partial_rope(fa["q"], fa["k_cache"], fa.get("cos"), fa.get("sin"), fa.get("rotary_dim", 64))
+        a = rnd(full_attention_decode(q, kc, fa["v_cache"], scale=fa.get("scale")))
+        if fa.get("out_proj") is not None:
+            a = rnd(a.reshape(a.shape[0], -1) @ as_f32(fa["out_proj"]).T)
+        a = a.reshape(h.shape)
+        res["attention_output"] = a
+        resid = rnd(h + a)
+    elif kind == "linear_attention":
+        if linear_attention is None:
+            raise ValueError("linear_attention inputs are required for linear_attention layers")
+        la = linear_attention
+        if la.get("g") is not None:
+            o, s = gated_delta_decode(la["q"], la["k"], la["v"], la["state"], la["g"], la["beta"])
+        else:
+            o, s = linear_attention_decode(la["q"], la["k"], la["v"], la["state"], decay=la.get("decay", 1.0))
+        o = rnd(o)
+        if la.get("out_proj") is not None:
+            o = rnd(o.reshape(o.shape[0], -1) @ as_f32(la["out_proj"]).T)
+        o = o.reshape(h.shape)
+        res["linear_output"] = o
+        res["linear_state"] = s
+        resid = rnd(h + o)
+    else:
+        raise ValueError(f"unsupported layer_type: {kind}")
+    if dense_ffn is not None:
+        d = dense_ffn
+        out = dense_ffn_decode(resid, d["norm_weight"], d["gate_weight"], d["up_weight"], d["down_weight"],
+                               eps=eps, add_residual=True)
+    else:
+        if moe is None:
+            raise ValueError("either moe or dense_ffn weights are required")
+        m = moe
+        out, idx, w = moe_decode(resid, m["norm_weight"], m["router_weight"], m["expert_gate"], m["expert_up"],
+                                 m["expert_down"], m["shared_gate"], m["shared_up"], m["shared_down"],
+                                 eps=eps, top_k=top_k, add_residual=True,
+                                 shared_expert_gate=m.get("shared_expert_gate"))
+        res["router_indices"] = idx
+        res["router_weights"] = w
+    res["hidden"] = out
+    return res
+
+
+# Which independent check pins each function (see tests/test_oracle.py).
+PINNING = {
+    "rms_norm": "torch.nn.functional.rms_norm (library); golden vectors (float64 torch)",
+    "topk_desc": "torch.topk on distinct values; tie rule (lower index first) by construction",
+    "moe_decode": "E=1,k=1 reduces to dense FFN + shared; identical experts => routed part independent "
+                  "of routing; w_sg=0 => shared factor 0.5; golden vectors (float64 torch composition)",
+    "dense_ffn_decode": "zero gate => out = x; F.linear/F.silu float64 composition; golden vectors",
+    "apply_partial_rope": "rotary_dim=0 / cos=1,sin=0 identity; norm preservation of rotated pairs",
+    "full_attention_decode": "F.scaled_dot_product_attention(enable_gqa=True); T=1 => out=v; constant K => mean(V)",
+    "linear_attention_decode": "decay=0 => S'=k v^T; closed-form o=(q.k) v + decay q^T S",
+    "gated_delta_decode": "beta=0 => S'=e^g S; g=0,beta=0 => S'=S; |k|=1,beta=1 => S'^T k = v; "
+                          "S=0,beta=1 => S'=k v^T; transformers' recurrent gated delta rule loop",
+    "decode_layer": "composition of pinned ops; dispatch errors match ops.py:720-739",
+}

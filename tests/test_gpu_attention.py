@@ -1,0 +1,96 @@
+"""GPU parity: GQA full-attention decode (split-K flash-decode on MFMA) vs the oracle.
+
+Tolerance (task): bf16 outputs atol 1e-2, rtol 1e-2.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import mega_kernel_qwen36 as mk
+import oracle
+from tests.inputs import assert_close_out, make_attention, np32
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(inp):
+    return oracle.full_attention_decode(np32(inp.q), np32(inp.k_cache), np32(inp.v_cache), scale=inp.scale)
+
+
+@pytest.mark.parametrize("seq_len", [1, 128, 4096])
+def test_attention_reference_test_shape(seq_len):
+    # test_cuda_ops.py:79-90 shape: B 2, Hq 4, Hkv 2, D 32, values * 0.1
+    inp = make_attention(batch=2, q_heads=4, kv_heads=2, head_dim=32, seq_len=seq_len, seed=17, scale=0.1)
+    out = mk.full_attention_decode(inp)
+    assert out.shape == inp.q.shape and out.dtype == inp.q.dtype
+    assert_close_out(out, _ref(inp))
+
+
+@pytest.mark.parametrize("seq_len", [4096, 32768])
+def test_attention_config4(seq_len):
+    """Config 4: B 1, 24 q heads, 4 kv heads, D 256, contiguous bf16 KV."""
+    inp = make_attention(seq_len=seq_len)
+    assert_close_out(mk.full_attention_decode(inp), _ref(inp))
+
+
+def test_attention_config4_128k():
+    inp = make_attention(seq_len=131072)
+    assert_close_out(mk.full_attention_decode(inp), _ref(inp))
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 24, 4, 256, 1000),   # ragged tail
+    (3, 6, 6, 128, 77),      # MHA (group 1)
+    (1, 32, 1, 64, 300),     # group 32 -> two head groups
+    (2, 8, 2, 40, 50),       # head_dim 40: 8-multiple, partial MFMA step
+    (1, 4, 2, 20, 33),       # head_dim 20: generic path
+])
+def test_attention_odd_shapes(shape):
+    b, hq, hkv, d, t = shape
+    inp = make_attention(batch=b, q_heads=hq, kv_heads=hkv, head_dim=d, seq_len=t, seed=sum(shape))
+    assert_close_out(mk.full_attention_decode(inp), _ref(inp))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_attention_other_dtypes(dtype):
+    inp = make_attention(batch=1, q_heads=12, kv_heads=2, head_dim=128, seq_len=2000, seed=5, dtype=dtype)
+    out = mk.full_attention_decode(inp)
+    assert out.dtype == dtype
+    assert_close_out(out, _ref(inp))
+
+
+def test_attention_known_answers():
+    # T = 1 => out = v ; constant keys => out = mean(V)
+    inp = make_attention(batch=1, q_heads=6, kv_heads=1, head_dim=256, seq_len=1, seed=8)
+    out = mk.full_attention_decode(inp)
+    expect = np32(inp.v_cache)[:, 0, 0][:, None, :].repeat(6, axis=1)
+    assert_close_out(out, expect)
+    inp = make_attention(batch=1, q_heads=6, kv_heads=1, head_dim=256, seq_len=513, seed=9)
+    k_const = inp.k_cache[:, :1].expand_as(inp.k_cache).contiguous()
+    out = mk.full_attention_decode(mk.FullAttentionInputs(q=inp.q, k_cache=k_const, v_cache=inp.v_cache))
+    expect = np32(inp.v_cache).mean(axis=1)[:, 0][:, None, :].repeat(6, axis=1)
+    assert_close_out(out, expect)
+
+
+def test_attention_default_scale_and_rope():
+    inp = make_attention(batch=1, q_heads=8, kv_heads=2, head_dim=64, seq_len=200, seed=10)
+    cos = torch.cos(torch.linspace(0, 3, 32)).repeat(2)[None].expand(200, 64)[:, :32].contiguous()
+    sin = torch.sin(torch.linspace(0, 3, 32)).repeat(2)[None].expand(200, 64)[:, :32].contiguous()
+    full = mk.FullAttentionInputs(q=inp.q, k_cache=inp.k_cache, v_cache=inp.v_cache, cos=cos[:1], sin=sin[:1],
+                                  rotary_dim=32)
+    out = mk.full_attention_decode(full)
+    qn, kn = oracle.apply_partial_rope(np32(inp.q), np32(inp.k_cache), cos[:1].numpy(), sin[:1].numpy(), 32)
+    # the API rounds the rotated q/k back to bf16 before the kernel, as the reference does
+    qn, kn = oracle.bf16_round(qn), oracle.bf16_round(kn)
+    ref = oracle.full_attention_decode(qn, kn, np32(inp.v_cache), scale=1.0 / math.sqrt(64))
+    assert_close_out(out, ref)
+
+
+def test_attention_deterministic():
+    inp = make_attention(batch=1, seq_len=8192, seed=12)
+    a = mk.full_attention_decode(inp)
+    b = mk.full_attention_decode(inp)
+    assert torch.equal(a, b)

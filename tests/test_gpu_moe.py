@@ -1,0 +1,144 @@
+"""GPU parity: persistent MoE decode (one HIP launch) vs the CPU oracle.
+
+Task tolerances: top-k indices bit-exact; router weights and bf16 outputs
+atol 1e-2 / rtol 1e-2 against the oracle run on FP32 upcasts of the inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import mega_kernel_qwen36 as mk
+import oracle
+from tests.inputs import assert_close_out, make_moe, moe_oracle_args, small_moe_reference_shape
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(x, w, k, add_residual=True):
+    args, sg = moe_oracle_args(x, w)
+    return oracle.moe_decode(*args, top_k=k, add_residual=add_residual, shared_expert_gate=sg)
+
+
+def _topk_margin(x, w, k):
+    """Gap between the k-th and (k+1)-th router logit per row (oracle arithmetic)."""
+    args, _ = moe_oracle_args(x, w)
+    xn = oracle.rms_norm(args[0], args[1])
+    logits = np.sort(xn @ args[2].T, axis=-1)[:, ::-1]
+    if logits.shape[1] <= k:
+        return np.inf
+    return float(np.min(logits[:, k - 1] - logits[:, k]))
+
+
+def _check(x, w, k, backend="persistent", add_residual=True):
+    out, idx, rw = mk.moe_decode(x, w, top_k=k, backend=backend, add_residual=add_residual)
+    ref, ref_idx, ref_w = _oracle(x, w, k, add_residual)
+    assert out.shape == x.shape and out.dtype == x.dtype
+    assert idx.dtype == torch.int64 and rw.dtype == torch.float32
+    assert idx.cpu().tolist() == ref_idx.tolist()
+    assert_close_out(rw, ref_w)
+    assert_close_out(out, ref)
+    return out, idx, rw
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+@pytest.mark.parametrize("backend", ["auto", "persistent"])
+def test_moe_reference_test_shape(batch, backend):
+    # test_cuda_ops.py:23-36: _small_moe shape (H 16, E 6, I 12, k 3), row 0 replicated
+    x, w, k = small_moe_reference_shape()
+    x = x[:1].repeat(batch, 1).contiguous()
+    _check(x, w, k, backend)
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_moe_config1_small(batch):
+    """Config 1 shape: H 512, E 8, top-2, I 256, shared 256 with a sigmoid gate."""
+    x, w, k = make_moe(batch=batch, hidden=512, experts=8, intermediate=256, shared_intermediate=256, top_k=2, seed=1)
+    _check(x, w, k)
+
+
+def test_moe_config1_fp32():
+    x, w, k = make_moe(batch=1, hidden=512, experts=8, intermediate=256, shared_intermediate=256, top_k=2, seed=1,
+                       dtype=torch.float32)
+    _check(x, w, k)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+def test_moe_config2(batch):
+    """Config 2: 35B-A3B MoE layer, independent rows, gated shared expert."""
+    x, w, k = make_moe(batch=batch)
+    assert _topk_margin(x, w, k) > 1e-4
+    _check(x, w, k)
+
+
+def test_moe_config2_replicated_rows():
+    x, w, k = make_moe(batch=4, replicate_rows=True)
+    _, idx, _ = _check(x, w, k)
+    assert all(row == idx[0].tolist() for row in idx.tolist())
+
+
+def test_moe_batch_over_eight():
+    x, w, k = make_moe(batch=11, hidden=256, experts=32, intermediate=128, shared_intermediate=64, top_k=4, seed=6)
+    _check(x, w, k)
+
+
+@pytest.mark.parametrize("add_residual", [False])
+def test_moe_no_residual_ungated(add_residual):
+    x, w, k = make_moe(batch=3, hidden=1024, experts=64, intermediate=256, shared_intermediate=384, top_k=6,
+                       gated=False, seed=2)
+    _check(x, w, k, add_residual=add_residual)
+
+
+def test_moe_fp16():
+    x, w, k = make_moe(batch=2, hidden=1024, experts=32, intermediate=512, shared_intermediate=512, top_k=4, seed=3,
+                       dtype=torch.float16)
+    _check(x, w, k)
+
+
+def test_moe_rejects_mixed_weight_dtype():
+    # test_cuda_ops.py:52-65
+    x, w, k = small_moe_reference_shape()
+    mixed = mk.MoeWeights(
+        norm_weight=w.norm_weight, router_weight=w.router_weight, expert_gate=w.expert_gate.float(),
+        expert_up=w.expert_up, expert_down=w.expert_down, shared_gate=w.shared_gate, shared_up=w.shared_up,
+        shared_down=w.shared_down)
+    with pytest.raises(RuntimeError, match="expert_gate dtype mismatch"):
+        mk.moe_decode(x, mixed, top_k=k, backend="persistent")
+
+
+def test_moe_deterministic_and_repeated_launches():
+    # back-to-back launches exercise the flag generations; results must be bit-identical
+    x, w, k = make_moe(batch=2)
+    first = mk.moe_decode(x, w, top_k=k)
+    for _ in range(20):
+        again = mk.moe_decode(x, w, top_k=k)
+        assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1]) and torch.equal(first[2], again[2])
+    # interleave another shape on the same stream/workspace, then come back
+    xs, ws, ks = small_moe_reference_shape()
+    _check(xs, ws, ks)
+    again = mk.moe_decode(x, w, top_k=k)
+    assert torch.equal(first[0], again[0])
+
+
+def test_moe_grouped_backend_agrees():
+    x, w, k = make_moe(batch=2, hidden=512, experts=16, intermediate=256, shared_intermediate=256, top_k=4, seed=4)
+    out, idx, rw = mk.moe_decode(x, w, top_k=k)
+    g_out, g_idx, g_rw = mk.moe_decode(x, w, top_k=k, backend="grouped")
+    assert idx.tolist() == g_idx.tolist()
+    torch.testing.assert_close(out.float(), g_out.float(), atol=3e-2, rtol=3e-2)
+
+
+def test_moe_cuda_graph_replay():
+    x, w, k = make_moe(batch=1)
+    eager = mk.moe_decode(x, w, top_k=k)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        captured = mk.moe_decode(x, w, top_k=k)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured[0], eager[0]) and torch.equal(captured[1], eager[1])
+        again = mk.moe_decode(x, w, top_k=k)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(again[0], eager[0])

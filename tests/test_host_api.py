@@ -1,0 +1,150 @@
+"""CPU tests of the boundary: the C ABI library, the Python API's host logic,
+error behaviour and configs.  No GPU is touched (the C entry points are only
+called with arguments their validation rejects before any HIP call)."""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+import mega_kernel_qwen36 as mk
+from mega_kernel_qwen36 import _lib
+
+REPO = pathlib.Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "mkq.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mkq_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.library_path()))
+    names = header_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in include/mkq.h but not exported"
+
+
+def test_ctypes_signatures_mirror_header():
+    assert sorted(_lib.SIGNATURES) == header_functions()
+
+
+def test_abi_version_and_error_string():
+    lib = _lib.load_library()
+    assert lib.mkq_abi_version() == 100
+    assert isinstance(lib.mkq_last_error(), bytes)
+
+
+def test_c_abi_rejects_bad_arguments_without_gpu():
+    lib = _lib.load_library()
+    rc = lib.mkq_dense_ffn_decode(_lib.MKQ_DTYPE_BF16, None, None, None, None, None, None, 0, 16, 16, 1e-6, 1,
+                                  None, 0, None)
+    assert rc == _lib.MKQ_ERR_INVALID
+    assert b"sizes must be positive" in lib.mkq_last_error()
+    rc = lib.mkq_moe_decode(_lib.MKQ_DTYPE_BF16, *([None] * 13), 1, 16, 4, 8, 8, 5, 1e-6, 1, None, 0, None)
+    assert rc == _lib.MKQ_ERR_INVALID
+    assert b"top_k must be in [1, experts]" in lib.mkq_last_error()
+    rc = lib.mkq_full_attention_decode(_lib.MKQ_DTYPE_BF16, None, None, None, None, 1, 6, 4, 64, 8, 1.0, None, 0,
+                                       None)
+    assert rc == _lib.MKQ_ERR_INVALID
+    assert b"query_heads must be divisible by kv_heads" in lib.mkq_last_error()
+    rc = lib.mkq_full_attention_decode(_lib.MKQ_DTYPE_BF16, None, None, None, None, 1, 4, 4, 512, 8, 1.0, None, 0,
+                                       None)
+    assert b"head_dim > 256" in lib.mkq_last_error()
+    rc = lib.mkq_gated_delta_decode(_lib.MKQ_DTYPE_BF16, *([None] * 8), 1, 3, 4, 8, 8, None)
+    assert rc == _lib.MKQ_ERR_INVALID
+    assert b"multiple of k_heads" in lib.mkq_last_error()
+
+
+def test_workspace_sizes():
+    lib = _lib.load_library()
+    assert lib.mkq_dense_ffn_decode_workspace_bytes(2, 5120, 17408) == 2 * 17408 * 4
+    assert lib.mkq_moe_decode_workspace_bytes(1, 2048, 256, 512, 512, 8) > 8 * 8 * 512 * 4
+    assert lib.mkq_full_attention_decode_workspace_bytes(1, 24, 4, 256, 32768) >= 24 * 32768 * 4
+
+
+# ---------------------------------------------------------------------------
+# Python API host logic (reference ops.py behaviour)
+# ---------------------------------------------------------------------------
+
+def _tiny_moe():
+    g = torch.Generator().manual_seed(0)
+    r = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    return r(2, 8), mk.MoeWeights(r(8), r(4, 8), r(4, 6, 8), r(4, 6, 8), r(4, 8, 6), r(6, 8), r(6, 8), r(8, 6))
+
+
+def test_backend_validation_messages():
+    x, w = _tiny_moe()
+    with pytest.raises(ValueError, match="backend must be one of: auto, persistent, grouped, reference"):
+        mk.moe_decode(x, w, backend="nope")
+    dw = mk.DenseFfnWeights(torch.ones(8), torch.ones(4, 8), torch.ones(4, 8), torch.ones(8, 4))
+    with pytest.raises(ValueError, match="backend must be one of: auto, torch, triton, reference"):
+        mk.dense_ffn_decode(x, dw, backend="nope")
+
+
+def test_hip_backends_fail_loudly_on_cpu_tensors():
+    x, w = _tiny_moe()
+    with pytest.raises(RuntimeError, match="GPU|HIP extension"):
+        mk.moe_decode(x, w, top_k=2)
+    with pytest.raises(RuntimeError, match="GPU|HIP extension"):
+        mk.moe_decode(x, w, top_k=2, backend="persistent")
+    with pytest.raises(RuntimeError, match="test infrastructure"):
+        mk.moe_decode(x, w, top_k=2, backend="reference")
+    inp = mk.FullAttentionInputs(q=torch.randn(1, 4, 8), k_cache=torch.randn(1, 3, 2, 8), v_cache=torch.randn(1, 3, 2, 8))
+    with pytest.raises(RuntimeError, match="GPU|HIP extension"):
+        mk.full_attention_decode(inp)
+    bad = mk.FullAttentionInputs(q=torch.randn(1, 3, 8), k_cache=torch.randn(1, 3, 2, 8), v_cache=torch.randn(1, 3, 2, 8))
+    with pytest.raises(ValueError, match="query_heads must be divisible by kv_heads"):
+        mk.full_attention_decode(bad)
+
+
+def test_grouped_torch_backend_runs_on_cpu_and_agrees_with_oracle():
+    import oracle
+
+    x, w = _tiny_moe()
+    out, idx, rw = mk.moe_decode(x, w, top_k=2, backend="grouped")
+    ref, ref_idx, ref_w = oracle.moe_decode(*(t.numpy() for t in (x, *w.__dict__.values())), top_k=2)
+    assert idx.tolist() == ref_idx.tolist()
+    torch.testing.assert_close(out, torch.from_numpy(ref), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(rw, torch.from_numpy(ref_w))
+
+
+def test_decode_layer_dispatch_errors():
+    x, w = _tiny_moe()
+    with pytest.raises(ValueError, match="full_attention inputs are required"):
+        mk.decode_layer(3, x, w)
+    with pytest.raises(ValueError, match="linear_attention inputs are required"):
+        mk.decode_layer(0, x, w)
+    with pytest.raises(ValueError, match="unsupported layer_type"):
+        mk.decode_layer(0, x, w, layer_type="conv")
+    lin = mk.LinearAttentionInputs(q=torch.randn(2, 2, 4), k=torch.randn(2, 2, 4), v=torch.randn(2, 2, 4),
+                                   state=torch.zeros(2, 2, 4, 4))
+    with pytest.raises(RuntimeError):  # CPU tensors never fall back to a CPU path
+        mk.decode_layer(0, x, w, linear_attention=lin)
+
+
+def test_gated_weights_dataclass_keeps_reference_fields():
+    x, w = _tiny_moe()
+    gw = mk.GatedMoeWeights(*w.__dict__.values(), shared_expert_gate=torch.zeros(8))
+    assert isinstance(gw, mk.MoeWeights)
+    assert list(mk.MoeWeights.__dataclass_fields__) == [
+        "norm_weight", "router_weight", "expert_gate", "expert_up", "expert_down", "shared_gate", "shared_up",
+        "shared_down"]
+    assert len(w.__dict__) == 8  # rebuilt by MoeWeights(*w.__dict__.values()) in the reference tests
+
+
+def test_configs_match_published_dims():
+    c = mk.qwen36_35b_a3b_config()
+    assert (c.hidden_size, c.num_experts, c.num_experts_per_tok, c.moe_intermediate_size,
+            c.shared_expert_intermediate_size) == (2048, 256, 8, 512, 512)
+    assert (c.linear_num_key_heads, c.linear_num_value_heads, c.linear_key_head_dim, c.head_dim) == (16, 32, 128, 256)
+    d = mk.qwen36_27b_config()
+    assert (d.hidden_size, d.intermediate_size, d.num_attention_heads, d.num_key_value_heads) == (5120, 17408, 24, 4)
+    assert [mk.qwen36_layer_type(i) for i in range(8)] == ["linear_attention"] * 3 + ["full_attention"] + \
+        ["linear_attention"] * 3 + ["full_attention"]
+    assert c.rotary_dim == 64
