@@ -41,9 +41,9 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
   const int qh = vh / rep;
   const bool col_ok = j < dv;
 
-  for (int i = threadIdx.x; i < dk; i += kThreads) {
-    qs[i] = to_f(q[(size_t(b) * hk + qh) * dk + i]);
-    ks[i] = to_f(k[(size_t(b) * hk + qh) * dk + i]);
+  for (int i = threadIdx.x; i < kMaxKeyDim; i += kThreads) {  // zero past dk
+    qs[i] = i < dk ? to_f(q[(size_t(b) * hk + qh) * dk + i]) : 0.f;
+    ks[i] = i < dk ? to_f(k[(size_t(b) * hk + qh) * dk + i]) : 0.f;
   }
   float d = decay, bt = 1.0f;
   if constexpr (GATED) {
@@ -53,12 +53,18 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
   const float vj = col_ok ? to_f(v[(size_t(b) * hv + vh) * dv + j]) : 0.f;
   __syncthreads();
 
+  // One descriptor over this head's state: rows i >= dk fall past its end and
+  // read as zero, so all loads issue back to back with no branches.  Lanes
+  // past the last column use an out-of-range offset.
   const size_t base = (size_t(b) * hv + vh) * size_t(dk) * dv;
+  const rsrc_t srd = make_rsrc(state + base, uint32_t(size_t(dk) * dv * 4));
+  const rsrc_t swr = make_rsrc(new_state + base, uint32_t(size_t(dk) * dv * 4));
   float s[kRowsPerWave];
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; ++r) {
     const int i = wave + r * kWaves;
-    s[r] = (col_ok && i < dk) ? state[base + size_t(i) * dv + j] * d : 0.f;
+    const uint32_t off = col_ok ? uint32_t((i * dv + j) * 4) : 0xFFFFFFF0u;
+    s[r] = buf_loadf(srd, off) * d;
   }
 
   float add = vj;  // reference rule: S += k (x) v
@@ -67,7 +73,7 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r) {
       const int i = wave + r * kWaves;
-      if (i < dk) p = fmaf(s[r], ks[i], p);
+      p = fmaf(s[r], ks[i], p);
     }
     red[wave][lane] = p;
     __syncthreads();
@@ -82,11 +88,11 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; ++r) {
     const int i = wave + r * kWaves;
-    if (i < dk) {
-      s[r] = fmaf(ks[i], add, s[r]);
-      o = fmaf(s[r], qs[i], o);
-      if (col_ok) new_state[base + size_t(i) * dv + j] = s[r];
-    }
+    // ks/qs are zero past dk, so rows i >= dk add nothing; their stores fall
+    // past the descriptor and are dropped.
+    s[r] = fmaf(ks[i], add, s[r]);
+    o = fmaf(s[r], qs[i], o);
+    buf_storef(swr, col_ok ? uint32_t((i * dv + j) * 4) : 0xFFFFFFF0u, s[r]);
   }
   red[wave][lane] = o;
   __syncthreads();

@@ -119,6 +119,41 @@ __device__ __forceinline__ u32x4 load_chunk(const T* __restrict__ row, int j, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// buffer-resource loads: branch-free and bounds-checked by the hardware
+// ---------------------------------------------------------------------------
+// A raw buffer descriptor (stride 0) covers `bytes` bytes from `base`; loads
+// at offsets past the end return zero and stores there are dropped.  Code that
+// guards each load with a branch makes the compiler wait for every load at the
+// branch join; expressing the guard as the descriptor's size keeps all loads
+// of a row in flight at once.  Word 3 = 0x00020000 is the gfx9 raw-buffer
+// format word (32-bit data, no swizzle).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Cache-policy bits of a buffer access: bit 1 = nt (streaming, read once);
+// bit 4 = sc1, the policy of an agent-scope atomic load, which reads data
+// written by other XCDs in the same kernel coherently.
+constexpr int kAuxNone = 0;
+constexpr int kAuxStream = 2;
+constexpr int kAuxCoherent = 16;
+
+template <int AUX = kAuxNone>
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX));
+}
+template <int AUX = kAuxNone>
+__device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX);
+}
+__device__ __forceinline__ float buf_loadf(rsrc_t r, uint32_t off) { return __uint_as_float(buf_load4(r, off)); }
+__device__ __forceinline__ void buf_storef(rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)off, 0, 0);
+}
+
 // Streaming (read-once) variant for weights: non-temporal hint.
 template <typename T, bool VEC>
 __device__ __forceinline__ u32x4 load_chunk_nt(const T* __restrict__ row, int j, int n) {
@@ -159,6 +194,107 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += xor_lane(v, 16);
   v += xor_lane(v, 32);
   return v;
+}
+
+// Sum over all 64 lanes, returned as a wave-uniform value.  DPP within each
+// 16-lane row, then row_bcast:15 / row_bcast:31 carry the row sums into lane
+// 63, which is read out with readlane -- no LDS permute on the way.
+__device__ __forceinline__ float wave_sum_u(float v) {
+  v = row16_sum(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// (value, index) of the largest value over the wave, ties to the lower index;
+// returned wave-uniform.  DPP steps inside each 16-lane row, then the four row
+// results are compared through readlane.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp_step(float& v, int& i) {
+  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+  const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
+  const bool take = ov > v || (ov == v && oi < i);
+  v = take ? ov : v;
+  i = take ? oi : i;
+}
+__device__ __forceinline__ void wave_argmax_u(float& v, int& i) {
+  argmax_dpp_step<0xB1>(v, i);
+  argmax_dpp_step<0x4E>(v, i);
+  argmax_dpp_step<0x124>(v, i);
+  argmax_dpp_step<0x128>(v, i);
+  float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+  for (int r = 1; r < 4; ++r) {
+    const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
+    const int ri = __builtin_amdgcn_readlane(i, 16 * r);
+    if (rv > bv || (rv == bv && ri < bi)) {
+      bv = rv;
+      bi = ri;
+    }
+  }
+  v = bv;
+  i = bi;
+}
+
+// Order-preserving 32-bit key of a float: the unsigned order of the keys is
+// the numeric order of the values (negatives reversed).  0 is below every
+// key of a non-NaN value, so it can mark an empty slot.
+__device__ __forceinline__ uint32_t ord_key(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ord_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Unsigned max over all 64 lanes, returned wave-uniform (DPP inside rows,
+// row_bcast into lane 63, readlane); 0 is the identity.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0xB1, 0xF, 0xF, false)));
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x4E, 0xF, 0xF, false)));
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x124, 0xF, 0xF, false)));
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x128, 0xF, 0xF, false)));
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x142, 0xA, 0xF, false)));
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x143, 0xC, 0xF, false)));
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
+}
+
+// Order-preserving 64-bit key of (value, index): larger value first, then the
+// lower index.  A float's bits map to an unsigned integer with the same order
+// (negatives reversed); the low word holds ~index.
+__device__ __forceinline__ uint64_t rank_key(float v, int index) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t hi = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (uint64_t(hi) << 32) | uint64_t(~uint32_t(index));
+}
+__device__ __forceinline__ float key_value(uint64_t k) {
+  const uint32_t hi = uint32_t(k >> 32);
+  return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi);
+}
+__device__ __forceinline__ int key_index(uint64_t k) { return int(~uint32_t(k)); }
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t max_dpp_step(uint64_t k) {
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0, uint32_t(k >> 32), CTRL, 0xF, 0xF, false);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0, uint32_t(k), CTRL, 0xF, 0xF, false);
+  const uint64_t o = (uint64_t(hi) << 32) | lo;
+  return o > k ? o : k;
+}
+// Largest key over the wave, returned wave-uniform.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+  k = max_dpp_step<0xB1>(k);
+  k = max_dpp_step<0x4E>(k);
+  k = max_dpp_step<0x124>(k);
+  k = max_dpp_step<0x128>(k);
+  uint64_t best = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint64_t rk = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(k >> 32), 16 * r))) << 32) |
+                        uint32_t(__builtin_amdgcn_readlane(int(uint32_t(k)), 16 * r));
+    best = rk > best ? rk : best;
+  }
+  return best;
 }
 
 __device__ __forceinline__ float wave_max(float v) {

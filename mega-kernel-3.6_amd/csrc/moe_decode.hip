@@ -4,33 +4,32 @@
 //
 // Semantics of reference.py:16-62 (moe_decode_reference); replaces the
 // cooperative kernel of persistent_moe_decode.cu:229-581 and its host wrapper
-// :648-860.  One launch, one workgroup per CU, no grid barrier: the phases are
-// chained by per-workgroup flags in the workspace.
+// :648-860.  One launch, one workgroup (8 waves) per CU, no grid barrier.
 //
-//   phase 0  every WG: issue its router row and shared-expert gate/up rows;
-//            RMSNorm of x (FP32, recomputed per WG from L2) into LDS; router
-//            logits for its expert rows -> workspace; publish router flag;
-//            shared-expert act = silu(g)*u for its shared rows -> workspace.
-//   phase 1  wait until every WG's router flag is up; top-k (descending
-//            logit, ties to the lower index) + softmax per batch row, one
-//            wave per row, repeated in every WG so no result has to be sent
-//            back; distinct experts of the batch are listed in expert order.
-//   phase 2  issue the first group of routed gate/up rows AND the first group
-//            of down-projection rows of this WG's output rows (both known from
-//            the routing alone), then compute act = w_route * silu(g) * u for
-//            each (expert row, batch row using it); publish act flag.
-//   phase 3  wait until every WG's act flag is up; stage act and the shared
-//            act in LDS; out[b, h] for this WG's output rows = sum over experts
-//            (fixed order) + sigmoid gate * shared down + residual.
+//   phase 0  every WG issues x, its router row and its shared-expert gate/up
+//            rows; RMSNorm (FP32) into LDS; router logits of its rows and the
+//            shared-expert act of its rows are published.
+//   phase 1  one wave per batch row gathers all router logits, then top-k
+//            (descending logit, ties to the lower index) and softmax over the
+//            k logits.  Every WG repeats this, so nothing is sent back; the
+//            distinct experts of the batch are listed in expert order.
+//   phase 2  each wave issues its routed gate/up rows AND the down-projection
+//            rows of its WG's output rows (both known from the routing alone)
+//            before computing act = w_route * silu(g) * u, which it publishes.
+//   phase 3  the WG gathers act and the shared act into LDS and finishes its
+//            output rows: sum over experts (fixed order) + gate * shared
+//            down + residual.
 //
-// Cross-WG data (logits, act, shared act) is written and read with agent-scope
-// atomic accesses, which are coherent across the 8 XCD L2s without
-// invalidating them; each flag is published with a release store after the
-// data.  Flags carry a generation number that every launch derives from the
-// workspace itself (WG 0 advances it once all WGs have read it), so repeated
-// launches and graph replays need no host-side reset.  Spin-waits are bounded:
-// after kSpinLimit polls the kernel records an error code in the workspace
-// and finishes without waiting.
+// Hand-off between WGs: every published value is one 64-bit word {float bits,
+// generation tag}, written with a single agent-coherent store and read with
+// agent-coherent (sc1) loads, which see other XCDs' stores without any cache
+// invalidation.  A reader that sees the current tag has the current value (an
+// aligned 8-byte store is seen whole), so there are no flags, no fences and
+// no waits for store completion.  The tag is the workspace's generation word
+// + 1; every WG also publishes a tagged presence word, and WG 0 advances the
+// generation at its very end, once all presence words carry the tag (so every
+// WG has read it).  Repeated launches and graph replays need no reset.  Waits are bounded (kSpinLimit polls); on timeout the
+// kernel records an error code in the workspace, writes NaN and finishes.
 //
 // Every weight byte is read from HBM once per launch: router, shared expert,
 // and the gate/up/down rows of each distinct selected expert (once even when
@@ -45,23 +44,25 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kMaxB = 8;             // batch rows per launch (larger batches are split on the host)
-constexpr int kMaxWg = 1024;         // flag slots
-constexpr int kMaxHC = 8;            // max 16-byte chunks per lane for a hidden-long row (H <= 512*EPC)
-constexpr int kMaxIC = 2;            // max 16-byte chunks per lane for an intermediate-long row (I <= 128*EPC)
-constexpr int kGU = 2;               // routed gate/up row pairs in flight per wave
-constexpr int kDN = 8;               // down rows in flight per wave
+constexpr int kMaxB = 8;       // batch rows per launch (larger batches are split on the host)
+constexpr int kMaxWg = 1024;   // workgroups
+constexpr int kMaxHC = 8;      // max 16-byte chunks per lane for a hidden-long row (H <= 512*EPC)
+constexpr int kMaxIC = 2;      // max 16-byte chunks per lane for an intermediate-long row (I <= 128*EPC)
+constexpr int kGU = 2;         // routed gate/up row pairs in flight per wave
+constexpr int kDN = 8;         // down rows in flight per wave
+constexpr int kMaxEL = 16;     // router logits per lane (E <= 1024)
 constexpr int kActWindowBytes = 64 * 1024;
-constexpr unsigned kSpinLimit = 1u << 22;
+constexpr unsigned kSpinLimit = 1u << 21;
 
-// Workspace layout (bytes).
-constexpr size_t kOffGen = 0;          // uint32 generation
-constexpr size_t kOffErr = 4;          // uint32 error code (1 = spin limit hit)
-constexpr size_t kOffRFlag = 256;      // uint32[kMaxWg]
-constexpr size_t kOffAFlag = kOffRFlag + 4 * kMaxWg;
-constexpr size_t kOffData = kOffAFlag + 4 * kMaxWg;
+// Workspace layout (bytes).  The generation and error words live in their own
+// 256-byte lines; the tagged arrays follow, each 256-byte aligned.
+constexpr size_t kOffGen = 0;                         // uint32 generation
+constexpr size_t kOffErr = 256;                       // uint32 error code (1 = a wait timed out)
+constexpr size_t kOffPresence = 512;                  // uint64[kMaxWg] tagged
+constexpr size_t kOffData = kOffPresence + 8 * kMaxWg;
 
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
+__host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 template <typename T>
 struct MoeArgs {
@@ -89,100 +90,135 @@ struct MoeArgs {
 struct WsPtrs {
   unsigned* gen;
   unsigned* err;
-  unsigned* rflag;
-  unsigned* aflag;
-  float* logits;  // [B][E]
-  float* act;     // [B*K][I]   (b, slot) entries, route weight folded in
-  float* sact;    // [B][Is]
+  uint64_t* presence;  // [nwg]   tagged
+  uint64_t* logits;  // [B][E]        tagged
+  uint64_t* act;     // [B*K][I]      tagged, (b, slot) rows, route weight folded in
+  uint64_t* sact;    // [B][Is]       tagged
 };
 
-__host__ __device__ inline WsPtrs ws_ptrs(unsigned char* ws, int B, int E, int I, int K) {
+__host__ __device__ inline WsPtrs ws_ptrs(unsigned char* ws, int E, int I, int Is, int K) {
   WsPtrs p;
   p.gen = reinterpret_cast<unsigned*>(ws + kOffGen);
   p.err = reinterpret_cast<unsigned*>(ws + kOffErr);
-  p.rflag = reinterpret_cast<unsigned*>(ws + kOffRFlag);
-  p.aflag = reinterpret_cast<unsigned*>(ws + kOffAFlag);
-  p.logits = reinterpret_cast<float*>(ws + kOffData);
-  p.act = p.logits + size_t(B) * E;
-  p.sact = p.act + size_t(B) * K * I;
+  p.presence = reinterpret_cast<uint64_t*>(ws + kOffPresence);
+  size_t off = kOffData;
+  p.logits = reinterpret_cast<uint64_t*>(ws + off);
+  off = align256(off + 8 * size_t(kMaxB) * E);
+  p.act = reinterpret_cast<uint64_t*>(ws + off);
+  off = align256(off + 8 * size_t(kMaxB) * K * I);
+  p.sact = reinterpret_cast<uint64_t*>(ws + off);
+  (void)Is;
   return p;
 }
 
-__device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__host__ __device__ inline size_t ws_bytes(int E, int I, int Is, int K) {
+  size_t off = kOffData;
+  off = align256(off + 8 * size_t(kMaxB) * E);
+  off = align256(off + 8 * size_t(kMaxB) * K * I);
+  off = align256(off + 8 * size_t(kMaxB) * Is);
+  return off;
 }
 
-// Wave-level wait until flags[0..n) all equal `tag` (bounded).  Returns false
-// on timeout.  Followed by a workgroup-scope acquire fence, so later loads are
-// issued only after the flags were seen; the data itself is read with
-// agent-scope atomic loads.
-__device__ bool wait_flags(unsigned* flags, int n, unsigned tag, int lane) {
-  unsigned polls = 0;
-  while (true) {
-    bool ok = true;
-    for (int i = lane; i < n; i += kWave) {
-      const unsigned f = __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = ok && (f == tag);
-    }
-    if (__all(ok)) break;
-    if (++polls >= kSpinLimit) return false;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  return true;
+// One agent-coherent 64-bit store of {value, tag}.
+__device__ __forceinline__ void put_tagged(uint64_t* p, float v, unsigned tag) {
+  const uint64_t word = (uint64_t(tag) << 32) | uint64_t(__float_as_uint(v));
+  __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2 ld8_coherent(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kAuxCoherent));
 }
 
 // Loads up to MAXC 16-byte chunks per lane of a row of length n (chunk j of
-// the lane is chunk lane + 64*j of the row); chunks past the row read as 0.
+// the lane is chunk lane + 64*j of the row); chunks past the row, and every
+// chunk of a row with valid == false, read as 0.  The vector path uses one
+// buffer descriptor sized to the row, so there is no branch around the loads
+// and all of them stay in flight together.
 template <typename T, bool VEC, int MAXC>
-__device__ __forceinline__ void load_row(const T* __restrict__ row, int n, int lane, u32x4 (&c)[MAXC]) {
+__device__ __forceinline__ void load_row(const T* __restrict__ row, int n, bool valid, int lane, u32x4 (&c)[MAXC]) {
   constexpr int EPC = Epc<T>::value;
-  const int nch = (n + EPC - 1) / EPC;
+  if constexpr (VEC) {
+    const rsrc_t r = make_rsrc(row, valid ? uint32_t(n) * uint32_t(sizeof(T)) : 0u);
 #pragma unroll
-  for (int j = 0; j < MAXC; ++j) {
-    const int q = lane + kWave * j;
-    c[j] = q < nch ? load_chunk_nt<T, VEC>(row, q, n) : u32x4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < MAXC; ++j) c[j] = buf_load16<kAuxStream>(r, uint32_t(lane + kWave * j) * 16u);
+  } else {
+    const int nch = (n + EPC - 1) / EPC;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+      const int q = lane + kWave * j;
+      c[j] = (valid && q < nch) ? load_chunk<T, false>(row, q, n) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 }
 
 // Lane-partial dot of the chunks with an FP32 vector in LDS (zero-padded to a
-// multiple of EPC).
+// multiple of EPC).  Branch-free: a chunk past the row was loaded as zeros,
+// so it is multiplied with the (finite) last chunk of the vector instead of
+// being skipped.
 template <typename T, int MAXC>
 __device__ __forceinline__ float dot_row(const u32x4 (&c)[MAXC], const float* __restrict__ v, int n, int lane) {
   constexpr int EPC = Epc<T>::value;
-  const int nch = (n + EPC - 1) / EPC;
+  const int last = (n + EPC - 1) / EPC - 1;
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < MAXC; ++j) {
-    const int q = lane + kWave * j;
-    if (q < nch) {
-      float f[EPC];
-      unpack(c[j], f, T{});
+    const int q = min(lane + kWave * j, last);
+    float f[EPC];
+    unpack(c[j], f, T{});
 #pragma unroll
-      for (int e = 0; e < EPC; ++e) s = fmaf(f[e], v[q * EPC + e], s);
-    }
+    for (int e = 0; e < EPC; ++e) s = fmaf(f[e], v[q * EPC + e], s);
   }
   return s;
 }
 
-// Wave argmax over (value desc, index asc).
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+// Gathers `pairs` pairs of tagged words (word 2p, 2p+1 of the array behind
+// `r`, pair p taken from pair index src(p)) into `dst` floats, waiting until
+// every word carries `tag`.  Each thread waits only for its own words; the
+// caller's barrier then makes the whole set visible to the workgroup.
+// Returns false on timeout.
+template <typename SrcFn>
+__device__ bool gather_tagged_pairs(rsrc_t r, int pairs, SrcFn src, float* dst, unsigned tag, int tid) {
+  bool ok = true;
+  for (int f0 = tid; f0 < pairs; f0 += 4 * kThreads) {
+    u32x4 v[4];
+    uint32_t off[4];
 #pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) {
-    const float ov = __shfl_xor(v, m, kWave);
-    const int oi = __shfl_xor(i, m, kWave);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
+    for (int q = 0; q < 4; ++q) {
+      const int f = f0 + q * kThreads;
+      off[q] = f < pairs ? src(f) : 0xFFFFFFF0u;
+    }
+    unsigned polls = 0;
+    while (true) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = buf_load16<kAuxCoherent>(r, off[q]);
+      bool ready = true;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        ready = ready & (off[q] == 0xFFFFFFF0u || (v[q].y == tag && v[q].w == tag));
+      if (ready) break;
+      if (++polls >= kSpinLimit) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int f = f0 + q * kThreads;
+      if (f < pairs) {
+        dst[2 * f] = __uint_as_float(v[q].x);
+        dst[2 * f + 1] = __uint_as_float(v[q].z);
+      }
     }
   }
+  return ok;
 }
 
 // HC / IC: 16-byte chunks per lane of a hidden-long / intermediate-long row.
-template <typename T, bool VEC, int HC, int IC>
+// MB: largest batch of this instantiation (1 = the single-token fast path).
+// EL: router logits held per lane in the top-k (E <= 64*EL).
+template <typename T, bool VEC, int HC, int IC, int MB, int EL>
 __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   constexpr int EPC = Epc<T>::value;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -190,188 +226,292 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   const int wg = blockIdx.x, nwg = a.nwg;
   const int B = a.B, H = a.H, E = a.E, I = a.I, Is = a.Is, K = a.K;
   const int Hp = round_up(H, EPC), Ip = round_up(I, EPC), Isp = round_up(Is, EPC);
-  const WsPtrs w = ws_ptrs(a.ws, B, E, I, K);
+  const WsPtrs w = ws_ptrs(a.ws, E, I, Is, K);
 
   // ---- LDS carve-up --------------------------------------------------------
-  // region A (phases 0-2): x_norm [B][Hp] ; region A reused in phase 3 for the
-  // act window and the shared act.  Small bookkeeping arrays follow.
+  // region A: x_norm [B][Hp] (phases 0-2); reused in phase 3 for the act
+  // window [entries][Ip] and the shared act [B][Isp].
   const int ulimit = min(E, B * K);
   float* xn = reinterpret_cast<float*>(smem);
   const size_t region_a = size_t(max(B * Hp, kActWindowBytes / 4 + B * Isp));
-  float* act_l = xn;                        // [win entries][Ip]
-  float* sact_l = xn + kActWindowBytes / 4;  // [B][Isp]
-  float* red = xn + region_a;                // [kWaves][2*kMaxB]
-  float* sgf = red + kWaves * 2 * kMaxB;     // [kMaxB]
-  float* sel_w = sgf + kMaxB;                // [B*K]
-  int* sel_e = reinterpret_cast<int*>(sel_w + kMaxB * K);  // [B*K]
-  unsigned* emask = reinterpret_cast<unsigned*>(sel_e + kMaxB * K);  // [E]
+  float* act_l = xn;
+  float* sact_l = xn + kActWindowBytes / 4;
+  float* red = xn + region_a;                                        // [kWaves][2*MB]
+  float* sgf = red + kWaves * 2 * MB;                             // [MB]
+  float* sel_w = sgf + MB;                                        // [MB*K]
+  int* sel_e = reinterpret_cast<int*>(sel_w + MB * K);            // [MB*K]
+  unsigned* emask = reinterpret_cast<unsigned*>(sel_e + MB * K);  // [E]
   int* ulist = reinterpret_cast<int*>(emask + E);                    // [ulimit]
   unsigned* umask = reinterpret_cast<unsigned*>(ulist + ulimit);     // [ulimit]
-  int* uslot = reinterpret_cast<int*>(umask + ulimit);               // [ulimit][kMaxB]
-  int* misc = uslot + ulimit * kMaxB;                                // [0]=U, [1..kWaves] wave counts, [16] timeout
-  float* part = reinterpret_cast<float*>(misc + 32);                 // [rows_per_wg][U+1][B]
+  int* uslot = reinterpret_cast<int*>(umask + ulimit);               // [ulimit][MB]
+  int* ent_src = uslot + ulimit * MB;                             // [MB*K] act rows of a window
+  int* ent_of = ent_src + MB * K;                                 // [ulimit][MB] window entry of (u, b)
+  int* misc = ent_of + ulimit * MB;                               // [0]=U, [1..kWaves] counts, [16] error
+  float* part = reinterpret_cast<float*>(misc + 32);                 // [rows_per_wg][MB] running sums
 
+  // ---- phase 0 -------------------------------------------------------------
+
+  // x and the norm weight first: loads complete in order, so the norm waits
+  // only for these, not for the weight rows issued after them.
+  const int hq = Hp / EPC;
+  u32x4 xc[4], nc[4], gc[4];
+  const rsrc_t gsr = make_rsrc(a.wsg, a.wsg != nullptr ? uint32_t(H) * uint32_t(sizeof(T)) : 0u);
+  if constexpr (VEC) {
+    const rsrc_t xr = make_rsrc(a.x, uint32_t(B) * uint32_t(H) * uint32_t(sizeof(T)));
+    const rsrc_t nr = make_rsrc(a.nw, uint32_t(H) * uint32_t(sizeof(T)));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int q = tid + r * kThreads;
+      xc[r] = buf_load16(xr, q < B * hq ? uint32_t(q) * 16u : 0xFFFFFFF0u);
+      nc[r] = buf_load16(nr, uint32_t(q % hq) * 16u);
+      gc[r] = buf_load16(gsr, uint32_t(q % hq) * 16u);
+    }
+  }
+  // Generation of this launch (advanced by WG 0 at the end of the previous
+  // one).  Loaded by every thread (no branch) after x, so the norm does not
+  // wait for it; the tag is first used after the norm.
   const unsigned gen = __hip_atomic_load(w.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned tag = gen + 1;
-
-  // ---- phase 0: issue router / shared gate-up rows --------------------------
   const int e0 = wg + nwg * wave;  // first router row of this wave
   u32x4 rrow[HC];
-  if (e0 < E) load_row<T, VEC, HC>(a.router + size_t(e0) * H, H, lane, rrow);
+  load_row<T, VEC, HC>(a.router + size_t(min(e0, E - 1)) * H, H, e0 < E, lane, rrow);
   const int s0 = wg + nwg * (kWaves - 1 - wave);  // first shared gate/up row of this wave
   u32x4 sgr[HC], sur[HC];
-  if (s0 < Is) {
-    load_row<T, VEC, HC>(a.sg + size_t(s0) * H, H, lane, sgr);
-    load_row<T, VEC, HC>(a.su + size_t(s0) * H, H, lane, sur);
-  }
+  load_row<T, VEC, HC>(a.sg + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sgr);
+  load_row<T, VEC, HC>(a.su + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sur);
+  // Shared-expert down row of this wave's first output row: independent of
+  // the routing, so it is fetched now, while HBM would otherwise idle.
+  const int h0 = wg * a.rows_per_wg;
+  const int nrows = max(0, min(a.rows_per_wg, H - h0));
+  u32x4 sdn[IC];
+  load_row<T, VEC, IC>(a.sd + size_t(min(h0 + wave, H - 1)) * Is, Is, wave < nrows, lane, sdn);
 
-  // RMSNorm (FP32) into LDS; x * nw first, then scaled by 1/rms.
-  if (tid < E) emask[tid] = 0u;
-  for (int e = tid + kThreads; e < E; e += kThreads) emask[e] = 0u;
+  if constexpr (MB > 1)
+    for (int e = tid; e < E; e += kThreads) emask[e] = 0u;
   {
-    float ss[kMaxB];
+    float ss[MB], gs[MB];
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b) ss[b] = 0.f;
-    for (int h = tid; h < Hp; h += kThreads) {
-      const float nwv = h < H ? to_f(a.nw[h]) : 0.f;
+    for (int b = 0; b < MB; ++b) ss[b] = gs[b] = 0.f;
+    if constexpr (VEC) {
+      // chunk q = (row q / hq, chunk q % hq); the first 4*512 chunks were
+      // loaded above, any beyond (B*H > 16384 elements) are loaded here.
+      for (int q0 = tid; q0 < B * hq; q0 += 4 * kThreads) {
+        if (q0 != tid) {
+          const rsrc_t xr = make_rsrc(a.x, uint32_t(B) * uint32_t(H) * uint32_t(sizeof(T)));
+          const rsrc_t nr = make_rsrc(a.nw, uint32_t(H) * uint32_t(sizeof(T)));
 #pragma unroll
-      for (int b = 0; b < kMaxB; ++b)
-        if (b < B) {
-          const float v = h < H ? to_f(a.x[size_t(b) * H + h]) : 0.f;
-          ss[b] = fmaf(v, v, ss[b]);
-          xn[b * Hp + h] = v * nwv;
+          for (int r = 0; r < 4; ++r) {
+            const int q = q0 + r * kThreads;
+            xc[r] = buf_load16(xr, q < B * hq ? uint32_t(q) * 16u : 0xFFFFFFF0u);
+            nc[r] = buf_load16(nr, uint32_t(q % hq) * 16u);
+          }
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int q = q0 + r * kThreads;
+          if (q < B * hq) {
+            const int b = q / hq, c = q % hq;
+            float xf[EPC], nf[EPC];
+            unpack(xc[r], xf, T{});
+            unpack(nc[r], nf, T{});
+            float sq = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+              sq = fmaf(xf[e], xf[e], sq);
+              xn[b * Hp + c * EPC + e] = xf[e] * nf[e];
+            }
+#pragma unroll
+            for (int bb = 0; bb < MB; ++bb) ss[bb] += bb == b ? sq : 0.f;
+          }
+        }
+      }
+    } else {
+      for (int h = tid; h < Hp; h += kThreads) {
+        const float nwv = h < H ? to_f(a.nw[h]) : 0.f;
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+          if (b < B) {
+            const float v = h < H ? to_f(a.x[size_t(b) * H + h]) : 0.f;
+            ss[b] = fmaf(v, v, ss[b]);
+            xn[b * Hp + h] = v * nwv;
+          }
+      }
     }
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b) {
-      const float t = wave_sum(ss[b]);
-      if (lane == 0) red[wave * 2 * kMaxB + b] = t;
+    for (int b = 0; b < MB; ++b) {
+      const float t = wave_sum_u(ss[b]);
+      if (lane == 0) red[wave * 2 * MB + b] = t;
     }
     __syncthreads();
-    float inv[kMaxB];
+    float inv[MB];
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b) {
+    for (int b = 0; b < MB; ++b) {
       float t = 0.f;
 #pragma unroll
-      for (int v = 0; v < kWaves; ++v) t += red[v * 2 * kMaxB + b];
+      for (int v = 0; v < kWaves; ++v) t += red[v * 2 * MB + b];
       inv[b] = 1.0f / sqrtf(t / float(H) + a.eps);
     }
-    float gs[kMaxB];
+    // Scale to x_norm in place; dot with the shared-expert gate vector.
+    if constexpr (VEC) {
+      for (int q0 = tid; q0 < B * hq; q0 += 4 * kThreads) {
+        if (q0 != tid) {  // the first 4*512 chunks' gate vector was loaded at the start
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b) gs[b] = 0.f;
-    for (int h = tid; h < Hp; h += kThreads) {
-      const float wg_ = (a.wsg != nullptr && h < H) ? to_f(a.wsg[h]) : 0.f;
-#pragma unroll
-      for (int b = 0; b < kMaxB; ++b)
-        if (b < B) {
-          const float v = xn[b * Hp + h] * inv[b];
-          xn[b * Hp + h] = v;
-          gs[b] = fmaf(v, wg_, gs[b]);
+          for (int r = 0; r < 4; ++r) gc[r] = buf_load16(gsr, uint32_t((q0 + r * kThreads) % hq) * 16u);
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int q = q0 + r * kThreads;
+          if (q < B * hq) {
+            const int b = q / hq, c = q % hq;
+            float gf[EPC];
+            unpack(gc[r], gf, T{});
+            float ib = 0.f;
+#pragma unroll
+            for (int bb = 0; bb < MB; ++bb) ib = bb == b ? inv[bb] : ib;
+            float dg = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+              const float v = xn[b * Hp + c * EPC + e] * ib;
+              xn[b * Hp + c * EPC + e] = v;
+              dg = fmaf(v, gf[e], dg);
+            }
+#pragma unroll
+            for (int bb = 0; bb < MB; ++bb) gs[bb] += bb == b ? dg : 0.f;
+          }
+        }
+      }
+    } else {
+      for (int h = tid; h < Hp; h += kThreads) {
+        const float wg_ = (a.wsg != nullptr && h < H) ? to_f(a.wsg[h]) : 0.f;
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+          if (b < B) {
+            const float v = xn[b * Hp + h] * inv[b];
+            xn[b * Hp + h] = v;
+            gs[b] = fmaf(v, wg_, gs[b]);
+          }
+      }
     }
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b) {
-      const float t = wave_sum(gs[b]);
-      if (lane == 0) red[wave * 2 * kMaxB + kMaxB + b] = t;
+    for (int b = 0; b < MB; ++b) {
+      const float t = wave_sum_u(gs[b]);
+      if (lane == 0) red[wave * 2 * MB + MB + b] = t;
     }
+    if (tid == 0) misc[16] = 0;
     __syncthreads();
     if (tid < B) {
       float t = 0.f;
-      for (int v = 0; v < kWaves; ++v) t += red[v * 2 * kMaxB + kMaxB + tid];
+      for (int v = 0; v < kWaves; ++v) t += red[v * 2 * MB + MB + tid];
       sgf[tid] = a.wsg != nullptr ? 1.0f / (1.0f + expf(-t)) : 1.0f;
     }
   }
+  const unsigned tag = gen + 1u;
+  if (tid == 0) put_tagged(w.presence + wg, 0.f, tag);
 
   // Router logits of this wave's rows.
   for (int e = e0, r = 0; e < E; e += nwg * kWaves, ++r) {
-    if (r > 0) load_row<T, VEC, HC>(a.router + size_t(e) * H, H, lane, rrow);
+    if (r > 0) load_row<T, VEC, HC>(a.router + size_t(e) * H, H, true, lane, rrow);
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b)
+    for (int b = 0; b < MB; ++b)
       if (b < B) {
-        const float s = wave_sum(dot_row<T, HC>(rrow, xn + b * Hp, H, lane));
-        if (lane == 0) st_agent(w.logits + size_t(b) * E + e, s);
+        const float s = wave_sum_u(dot_row<T, HC>(rrow, xn + b * Hp, H, lane));
+        if (lane == 0) put_tagged(w.logits + size_t(b) * E + e, s, tag);
       }
   }
-  // Each wave makes its own stores visible at agent scope before the barrier;
-  // only then does one thread raise the WG's flag.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (tid == 0) __hip_atomic_store(w.rflag + wg, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-
-  // Shared-expert gate/up of this wave's rows (published with the act flag).
+  // Shared-expert gate/up of this wave's rows.
   for (int s = s0, r = 0; s < Is; s += nwg * kWaves, ++r) {
     if (r > 0) {
-      load_row<T, VEC, HC>(a.sg + size_t(s) * H, H, lane, sgr);
-      load_row<T, VEC, HC>(a.su + size_t(s) * H, H, lane, sur);
+      load_row<T, VEC, HC>(a.sg + size_t(s) * H, H, true, lane, sgr);
+      load_row<T, VEC, HC>(a.su + size_t(s) * H, H, true, lane, sur);
     }
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b)
+    for (int b = 0; b < MB; ++b)
       if (b < B) {
-        const float g = wave_sum(dot_row<T, HC>(sgr, xn + b * Hp, H, lane));
-        const float u = wave_sum(dot_row<T, HC>(sur, xn + b * Hp, H, lane));
-        if (lane == 0) st_agent(w.sact + size_t(b) * Is + s, silu(g) * u);
+        const float g = wave_sum_u(dot_row<T, HC>(sgr, xn + b * Hp, H, lane));
+        const float u = wave_sum_u(dot_row<T, HC>(sur, xn + b * Hp, H, lane));
+        if (lane == 0) put_tagged(w.sact + size_t(b) * Is + s, silu(g) * u, tag);
       }
   }
 
-  // ---- phase 1: wait for all router logits, top-k ---------------------------
-  if (wave == 0) {
-    const bool ok = wait_flags(w.rflag, nwg, tag, lane);
-    if (lane == 0) misc[16] = ok ? 0 : 1;
-    if (!ok && lane == 0) __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  bool timed_out = misc[16] != 0;
-  if (wg == 0 && tid == 0 && !timed_out) {
-    // Every WG read `gen` before raising its router flag: advance it for the next launch.
-    __hip_atomic_store(w.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // ---- phase 1: gather the router logits, top-k -----------------------------
   if (wave < B) {
     const int b = wave;
-    constexpr int kMaxEL = 16;  // experts per lane (E <= 1024)
-    float v[kMaxEL];
+    const rsrc_t lr = make_rsrc(w.logits + size_t(b) * E, uint32_t(E) * 8u);
+    u32x2 word[EL];
+    unsigned polls = 0;
+    bool ok = true;
+    while (true) {
 #pragma unroll
-    for (int j = 0; j < kMaxEL; ++j) {
-      const int e = lane + kWave * j;
-      v[j] = (e < E && !timed_out) ? ld_agent(w.logits + size_t(b) * E + e) : -INFINITY;
-    }
-    unsigned taken = 0u;
-    float first = 0.f, denom = 0.f;
-    for (int s = 0; s < K; ++s) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
+      for (int j = 0; j < EL; ++j) word[j] = ld8_coherent(lr, uint32_t(lane + kWave * j) * 8u);
+      bool ready = true;
 #pragma unroll
-      for (int j = 0; j < kMaxEL; ++j) {
-        const int e = lane + kWave * j;
-        if (e < E && !((taken >> j) & 1u) && (v[j] > bv || (v[j] == bv && e < bi))) {
-          bv = v[j];
-          bi = e;
-        }
+      for (int j = 0; j < EL; ++j) ready = ready & (lane + kWave * j >= E || word[j].y == tag);
+      if (__all(ready)) break;
+      if (++polls >= kSpinLimit) {
+        ok = false;
+        break;
       }
-      wave_argmax(bv, bi);
-      if (bi < E && (bi & (kWave - 1)) == lane) taken |= 1u << (bi / kWave);
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok && lane == 0) {
+      misc[16] = 1;
+      __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Top-k: K rounds of a wave-wide max over order-preserving 32-bit keys of
+    // the logits (0 = absent/taken).  The winner's index is the lowest index
+    // holding the max key (ballot per key slot, slots in index order), which
+    // is the reference's tie rule.  Lane s keeps slot s.
+    uint32_t key[EL];
+#pragma unroll
+    for (int j = 0; j < EL; ++j) {
+      const int e = lane + kWave * j;
+      key[j] = (ok && e < E) ? ord_key(__uint_as_float(word[j].x)) : 0u;
+    }
+    float first = 0.f, denom = 0.f, my_w = 0.f;
+    int my_e = 0;
+    for (int s = 0; s < K; ++s) {
+      uint32_t lk = key[0];
+#pragma unroll
+      for (int j = 1; j < EL; ++j) lk = max(lk, key[j]);
+      const uint32_t best = wave_max_u32(lk);
+      // lowest index holding `best`: last matching slot wins going downward
+      int bi = -1;
+#pragma unroll
+      for (int j = EL - 1; j >= 0; --j) {
+        const unsigned long long m = __ballot(key[j] == best);
+        bi = m != 0ull ? kWave * j + int(__builtin_ctzll(m)) : bi;
+      }
+#pragma unroll
+      for (int j = 0; j < EL; ++j) key[j] = (kWave * j + lane == bi) ? 0u : key[j];
+      const float bv = ord_value(best);
       if (s == 0) first = bv;
       const float ex = expf(bv - first);
       denom += ex;
-      if (lane == 0) {
-        sel_e[b * K + s] = bi < E ? bi : 0;
-        sel_w[b * K + s] = ex;
+      if (lane == s) {
+        my_e = (bi >= 0 && bi < E) ? bi : 0;
+        my_w = ex;
       }
     }
-    if (lane == 0) {
-      const float inv = 1.0f / denom;
-      for (int s = 0; s < K; ++s) {
-        sel_w[b * K + s] *= inv;
-        atomicOr(&emask[sel_e[b * K + s]], 1u << b);
-        if (wg == 0) {
-          a.idx[size_t(b) * K + s] = sel_e[b * K + s];
-          a.wts[size_t(b) * K + s] = sel_w[b * K + s];
-        }
+    if (lane < K) {
+      my_w /= denom;
+      sel_e[b * K + lane] = my_e;
+      sel_w[b * K + lane] = my_w;
+      if constexpr (MB > 1) atomicOr(&emask[my_e], 1u << b);
+      if (wg == 0) {
+        a.idx[size_t(b) * K + lane] = my_e;
+        a.wts[size_t(b) * K + lane] = my_w;
       }
     }
   }
   __syncthreads();
-  // Compact the selected experts in expert order (ballot prefix per wave).
-  {
+  // Distinct experts of the batch.  One row: the K selected experts in slot
+  // order.  Several rows: compacted in expert order (ballot prefix per wave).
+  if constexpr (MB == 1) {
+    if (tid < K) {
+      ulist[tid] = sel_e[tid];
+      umask[tid] = 1u;
+    }
+    if (tid == 0) misc[0] = K;
+  } else {
     int cnt_before = 0;
     for (int base = 0; base < E; base += kThreads) {
       const int e = base + tid;
@@ -395,13 +535,18 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   }
   __syncthreads();
   const int U = misc[0];
+  bool timed_out = misc[16] != 0;
   // slot of expert u in batch row b (route weight lives in sel_w[b*K+slot]).
-  for (int t = tid; t < U * kMaxB; t += kThreads) {
-    const int u = t / kMaxB, b = t % kMaxB;
+  for (int t = tid; t < U * MB; t += kThreads) {
+    const int u = t / MB, b = t % MB;
     int slot = -1;
-    if (b < B)
-      for (int s = 0; s < K; ++s)
-        if (sel_e[b * K + s] == ulist[u]) slot = s;
+    if constexpr (MB == 1) {
+      slot = u;
+    } else {
+      if (b < B)
+        for (int s = 0; s < K; ++s)
+          if (sel_e[b * K + s] == ulist[u]) slot = s;
+    }
     uslot[t] = slot;
   }
   __syncthreads();
@@ -410,78 +555,102 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   const int nw_total = nwg * kWaves;
   const int gw = wave * nwg + wg;  // global wave id, consecutive ids on different WGs
   const int ntask = U * I;
-  // down pairs of this WG: (output row hl, expert u) for u < U, index p = hl*U + u
-  const int h0 = wg * a.rows_per_wg;
-  const int nrows = max(0, min(a.rows_per_wg, H - h0));
-  const int npairs = nrows * U;
+  // output rows of this WG in phase 3
 
-  u32x4 dn[kDN][IC];
+  // Task t = (expert u, row i) of the routed gate/up, t = gw + nw_total * m.
+  // Loads complete in issue order, so the first gate/up group is issued before
+  // the down rows: act is published as soon as its own rows arrive, while the
+  // down rows keep streaming during the hand-off.
+  const int step = nw_total * kGU;
+  auto issue_gu = [&](int t0, u32x4 (&g)[kGU][HC], u32x4 (&u)[kGU][HC]) {
 #pragma unroll
-  for (int j = 0; j < kDN; ++j) {
-    const int p = wave + kWaves * j;
-    if (p < npairs) {
-      const int hl = p / U, u = p % U;
-      load_row<T, VEC, IC>(a.ed + (size_t(ulist[u]) * H + h0 + hl) * I, I, lane, dn[j]);
+    for (int q = 0; q < kGU; ++q) {
+      const int t = t0 + q * nw_total;
+      const int tc = min(t, ntask - 1);
+      const size_t ro = (size_t(ulist[tc / I]) * I + tc % I) * H;
+      load_row<T, VEC, HC>(a.eg + ro, H, t < ntask, lane, g[q]);
+      load_row<T, VEC, HC>(a.eu + ro, H, t < ntask, lane, u[q]);
     }
-  }
-  // shared down row of this wave (one output row per wave, rest later)
-  u32x4 sdn[IC];
-  if (wave < nrows) load_row<T, VEC, IC>(a.sd + size_t(h0 + wave) * Is, Is, lane, sdn);
-
-  for (int t0 = gw; t0 < ntask; t0 += nw_total * kGU) {
-    u32x4 gr[kGU][HC], ur[kGU][HC];
+  };
+  auto compute_gu = [&](int t0, const u32x4 (&g)[kGU][HC], const u32x4 (&u)[kGU][HC]) {
 #pragma unroll
     for (int q = 0; q < kGU; ++q) {
       const int t = t0 + q * nw_total;
       if (t < ntask) {
-        const int u = t / I, i = t % I;
-        const size_t ro = (size_t(ulist[u]) * I + i) * H;
-        load_row<T, VEC, HC>(a.eg + ro, H, lane, gr[q]);
-        load_row<T, VEC, HC>(a.eu + ro, H, lane, ur[q]);
-      }
-    }
+        const int ue = t / I, i = t % I;
+        const unsigned mask = umask[ue];
 #pragma unroll
-    for (int q = 0; q < kGU; ++q) {
-      const int t = t0 + q * nw_total;
-      if (t < ntask) {
-        const int u = t / I, i = t % I;
-        const unsigned mask = umask[u];
-#pragma unroll
-        for (int b = 0; b < kMaxB; ++b)
+        for (int b = 0; b < MB; ++b)
           if ((mask >> b) & 1u) {
-            const float g = wave_sum(dot_row<T, HC>(gr[q], xn + b * Hp, H, lane));
-            const float u_ = wave_sum(dot_row<T, HC>(ur[q], xn + b * Hp, H, lane));
+            const float gv = wave_sum_u(dot_row<T, HC>(g[q], xn + b * Hp, H, lane));
+            const float uv = wave_sum_u(dot_row<T, HC>(u[q], xn + b * Hp, H, lane));
             if (lane == 0) {
-              const int slot = uslot[u * kMaxB + b];
-              const float rw = sel_w[b * K + slot];
-              st_agent(w.act + (size_t(b) * K + slot) * I + i, rw * silu(g) * u_);
+              const int slot = uslot[ue * MB + b];
+              put_tagged(w.act + (size_t(b) * K + slot) * I + i, sel_w[b * K + slot] * silu(gv) * uv, tag);
             }
           }
       }
     }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (tid == 0) __hip_atomic_store(w.aflag + wg, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  u32x4 gA[kGU][HC], uA[kGU][HC], gB[kGU][HC], uB[kGU][HC];
+  issue_gu(gw, gA, uA);
 
-  // ---- phase 3: wait for all act, down projection ---------------------------
-  if (wave == 0) {
-    const bool ok = timed_out ? false : wait_flags(w.aflag, nwg, tag, lane);
-    if (lane == 0) misc[17] = ok ? 0 : 1;
-    if (!ok && lane == 0) __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Double-buffered: the next group is in flight while this one is reduced.
+  for (int t0 = gw; t0 < ntask; t0 += 2 * step) {
+    if (t0 + step < ntask) issue_gu(t0 + step, gB, uB);
+    compute_gu(t0, gA, uA);
+    if (t0 + step >= ntask) break;
+    if (t0 + 2 * step < ntask) issue_gu(t0 + 2 * step, gA, uA);
+    compute_gu(t0 + step, gB, uB);
   }
-  __syncthreads();
-  timed_out = misc[17] != 0;
+  // Down rows of (output row h0 + wave, expert u = j), issued only now: they
+  // stream while act is handed over instead of competing with the gate/up
+  // rows on which act depends.
+  u32x4 dn[kDN][IC];
+#pragma unroll
+  for (int j = 0; j < kDN; ++j)
+    load_row<T, VEC, IC>(a.ed + (size_t(ulist[min(j, U - 1)]) * H + min(h0 + wave, H - 1)) * I, I,
+                         j < U && wave < nrows, lane, dn[j]);
+  __syncthreads();  // x_norm (region A) is dead from here on
 
-  // shared act -> LDS
-  for (int t = tid; t < B * Isp; t += kThreads) {
-    const int b = t / Isp, i = t % Isp;
-    sact_l[t] = (i < Is && !timed_out) ? ld_agent(w.sact + size_t(b) * Is + i) : 0.f;
+  // ---- phase 3: gather act, down projection --------------------------------
+  // shared act -> LDS [B][Isp]
+  bool ok3 = true;
+  if constexpr (VEC) {
+    const rsrc_t sr = make_rsrc(w.sact, uint32_t(B) * uint32_t(Is) * 8u);
+    const int hp = Isp / 2;  // word pairs per row
+    ok3 = gather_tagged_pairs(
+        sr, B * hp,
+        [&](int f) -> uint32_t {
+          const int b = f / hp, c2 = (f % hp) * 2;
+          return c2 < Is ? uint32_t(b * Is + c2) * 8u : 0xFFFFFFF0u;
+        },
+        sact_l, tag, tid);
+  } else {
+    for (int t = tid; t < B * Isp; t += kThreads) {
+      const int b = t / Isp, i = t % Isp;
+      float val = 0.f;
+      if (i < Is) {
+        uint64_t word = 0;
+        for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
+          word = __hip_atomic_load(w.sact + size_t(b) * Is + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (unsigned(word >> 32) == tag) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        ok3 = ok3 && unsigned(word >> 32) == tag;
+        val = __uint_as_float(unsigned(word));
+      }
+      sact_l[t] = val;
+    }
   }
-  // act windows: experts [u_lo, u_hi) whose (b, slot) entries fit the window
+  // Wave w owns output rows hl = w, w + kWaves, ...: it sums its experts in
+  // ascending expert order (wave-uniform values), keeping the running sums in
+  // part[hl][b] between act windows, then adds the gated shared expert and
+  // the residual and writes the row.  The down rows of (hl = w, expert u < kDN)
+  // were issued in phase 2.
+  for (int t = tid; t < a.rows_per_wg * MB; t += kThreads) part[t] = 0.f;
   const int win_entries = max(1, (kActWindowBytes / 4) / Ip);
-  int u_lo = 0, jdone = 0;
-  // entry index of (u, b) inside a window: running count of set mask bits
+  int u_lo = 0;
   while (u_lo < U) {
     int u_hi = u_lo, ent = 0;
     while (u_hi < U && (ent + __popc(umask[u_hi]) <= win_entries || u_hi == u_lo)) {
@@ -489,81 +658,122 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       ++u_hi;
     }
     __syncthreads();  // previous window fully consumed
-    // stage entries of experts [u_lo, u_hi): entry order = (u, b ascending)
-    for (int t = tid; t < ent * Ip; t += kThreads) {
-      const int en = t / Ip, i = t % Ip;
-      int u = u_lo, cnt = 0, bsel = 0;
-      for (; u < u_hi; ++u) {
-        const int pc = __popc(umask[u]);
-        if (en < cnt + pc) break;
-        cnt += pc;
-      }
-      unsigned m = umask[u];
-      for (int k2 = en - cnt; k2 > 0; --k2) m &= m - 1u;
-      bsel = __ffs(m) - 1;
-      const int slot = uslot[u * kMaxB + bsel];
-      act_l[t] = (i < I && !timed_out) ? ld_agent(w.act + (size_t(bsel) * K + slot) * I + i) : 0.f;
+    if (tid == 0) {
+      int en = 0;
+      for (int u = u_lo; u < u_hi; ++u)
+        for (int b = 0; b < MB; ++b)
+          if ((umask[u] >> b) & 1u) {
+            ent_src[en] = b * K + uslot[u * MB + b];
+            ent_of[u * MB + b] = en;
+            ++en;
+          }
     }
     __syncthreads();
-    // pairs of this window handled by this wave: p = wave + kWaves*j over all
-    // pairs (hl, u); only u in [u_lo, u_hi) are computed now.
-    for (int j = 0;; ++j) {
-      const int p = wave + kWaves * j;
-      if (p >= npairs) break;
-      const int hl = p / U, u = p % U;
-      if (u < u_lo || u >= u_hi) continue;
-      u32x4 c[IC];
-      if (j < kDN) {
-#pragma unroll
-        for (int jj = 0; jj < kDN; ++jj)
-          if (jj == j)
-#pragma unroll
-            for (int q = 0; q < IC; ++q) c[q] = dn[jj][q];
-      } else {
-        load_row<T, VEC, IC>(a.ed + (size_t(ulist[u]) * H + h0 + hl) * I, I, lane, c);
-      }
-      // window entry offset of expert u
-      int en = 0;
-      for (int v = u_lo; v < u; ++v) en += __popc(umask[v]);
-      const unsigned mask = umask[u];
-#pragma unroll
-      for (int b = 0; b < kMaxB; ++b)
-        if ((mask >> b) & 1u) {
-          const float s = wave_sum(dot_row<T, IC>(c, act_l + size_t(en) * Ip, I, lane));
-          if (lane == 0) part[(hl * (U + 1) + u) * kMaxB + b] = s;
-          ++en;
+    if constexpr (VEC) {
+      const rsrc_t ar = make_rsrc(w.act, uint32_t(B) * uint32_t(K) * uint32_t(I) * 8u);
+      const int hp = Ip / 2;
+      ok3 = gather_tagged_pairs(
+                ar, ent * hp,
+                [&](int f) -> uint32_t {
+                  const int en = f / hp, c2 = (f % hp) * 2;
+                  return c2 < I ? uint32_t(ent_src[en] * I + c2) * 8u : 0xFFFFFFF0u;
+                },
+                act_l, tag, tid) &&
+            ok3;
+    } else {
+      for (int t = tid; t < ent * Ip; t += kThreads) {
+        const int en = t / Ip, i = t % Ip;
+        float val = 0.f;
+        if (i < I) {
+          uint64_t word = 0;
+          const uint64_t* pw = w.act + size_t(ent_src[en]) * I + i;
+          for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
+            word = __hip_atomic_load(const_cast<uint64_t*>(pw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (unsigned(word >> 32) == tag) break;
+            __builtin_amdgcn_s_sleep(1);
+          }
+          ok3 = ok3 && unsigned(word >> 32) == tag;
+          val = __uint_as_float(unsigned(word));
         }
+        act_l[t] = val;
+      }
+    }
+    if (!ok3) misc[16] = 1;
+    __syncthreads();
+    for (int hl = wave; hl < nrows; hl += kWaves) {
+      float acc[MB];
+#pragma unroll
+      for (int b = 0; b < MB; ++b) acc[b] = part[hl * MB + b];
+      auto add_expert = [&](int u, const u32x4 (&c)[IC]) {
+        if constexpr (MB == 1) {  // one row: expert u's act is window entry u - u_lo
+          acc[0] += wave_sum_u(dot_row<T, IC>(c, act_l + size_t(u - u_lo) * Ip, I, lane));
+        } else {
+          const unsigned mask = umask[u];
+#pragma unroll
+          for (int b = 0; b < MB; ++b)
+            if ((mask >> b) & 1u)
+              acc[b] += wave_sum_u(dot_row<T, IC>(c, act_l + size_t(ent_of[u * MB + b]) * Ip, I, lane));
+        }
+      };
+      int u_next = u_lo;
+      if (hl == wave) {  // prefetched rows first (experts u < kDN, ascending)
+#pragma unroll
+        for (int uu = 0; uu < kDN; ++uu)
+          if (uu >= u_lo && uu < u_hi) add_expert(uu, dn[uu]);
+        u_next = max(u_lo, kDN);
+      }
+      for (int u = u_next; u < u_hi; ++u) {
+        u32x4 c[IC];
+        load_row<T, VEC, IC>(a.ed + (size_t(ulist[u]) * H + h0 + hl) * I, I, true, lane, c);
+        add_expert(u, c);
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) part[hl * MB + b] = acc[b];
+      }
     }
     u_lo = u_hi;
-    ++jdone;
   }
-  // shared down rows
+  __syncthreads();
+  timed_out = misc[16] != 0;
+  if (timed_out && tid == 0) __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // shared expert (gated) + residual; the owning wave writes its rows
   for (int hl = wave; hl < nrows; hl += kWaves) {
     u32x4 c[IC];
     if (hl == wave) {
 #pragma unroll
       for (int q = 0; q < IC; ++q) c[q] = sdn[q];
     } else {
-      load_row<T, VEC, IC>(a.sd + size_t(h0 + hl) * Is, Is, lane, c);
+      load_row<T, VEC, IC>(a.sd + size_t(h0 + hl) * Is, Is, true, lane, c);
     }
 #pragma unroll
-    for (int b = 0; b < kMaxB; ++b)
+    for (int b = 0; b < MB; ++b)
       if (b < B) {
-        const float s = wave_sum(dot_row<T, IC>(c, sact_l + b * Isp, Is, lane));
-        if (lane == 0) part[(hl * (U + 1) + U) * kMaxB + b] = s;
+        float s = fmaf(sgf[b], wave_sum_u(dot_row<T, IC>(c, sact_l + b * Isp, Is, lane)), part[hl * MB + b]);
+        const size_t o = size_t(b) * H + h0 + hl;
+        if (lane == 0) {
+          if (a.add_residual) s += to_f(a.x[o]);
+          a.out[o] = from_f<T>(timed_out ? NAN : s);
+        }
       }
   }
-  __syncthreads();
-  // combine: out[b, h] = sum_u part (expert order) + gate * shared + residual
-  for (int t = tid; t < nrows * B; t += kThreads) {
-    const int hl = t / B, b = t % B;
-    float s = 0.f;
-    for (int u = 0; u < U; ++u)
-      if ((umask[u] >> b) & 1u) s += part[(hl * (U + 1) + u) * kMaxB + b];
-    s = fmaf(sgf[b], part[(hl * (U + 1) + U) * kMaxB + b], s);
-    const size_t o = size_t(b) * H + h0 + hl;
-    if (a.add_residual) s += to_f(a.x[o]);
-    a.out[o] = from_f<T>(timed_out ? NAN : s);
+  // WG 0 advances the generation once every WG of this launch has read it.
+  if (wg == 0 && wave == 0) {
+    const rsrc_t pr = make_rsrc(w.presence, uint32_t(nwg) * 8u);
+    bool seen = false;
+    for (unsigned polls = 0; polls < kSpinLimit && !seen; ++polls) {
+      bool ready = true;
+      for (int q = lane; q < (nwg + 1) / 2; q += kWave) {
+        const u32x4 v = buf_load16<kAuxCoherent>(pr, uint32_t(q) * 16u);
+        ready = ready & (v.y == tag) & (2 * q + 1 >= nwg || v.w == tag);
+      }
+      seen = __all(ready);
+      if (!seen) __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) {
+      if (!seen) __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(w.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -573,9 +783,9 @@ size_t lds_bytes(int B, int H, int E, int I, int Is, int K, int epc, int rows_pe
   size_t region_a = size_t(B) * Hp;
   const size_t r3 = size_t(kActWindowBytes / 4) + size_t(B) * Isp;
   if (r3 > region_a) region_a = r3;
-  size_t n = region_a + kWaves * 2 * kMaxB + kMaxB + kMaxB * K;  // floats
-  n += kMaxB * K + E + ulimit + ulimit + size_t(ulimit) * kMaxB + 32;  // ints
-  n += size_t(rows_per_wg) * (ulimit + 1) * kMaxB;
+  size_t n = region_a + kWaves * 2 * kMaxB + kMaxB + kMaxB * K;                    // floats
+  n += kMaxB * K + E + ulimit + ulimit + size_t(ulimit) * kMaxB + kMaxB * K + size_t(ulimit) * kMaxB + 32;  // ints
+  n += size_t(rows_per_wg) * kMaxB;
   (void)I;
   return n * 4;
 }
@@ -585,31 +795,32 @@ int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
   constexpr int EPC = Epc<T>::value;
   MoeArgs<T> a = args0;
   const int ncu = cu_count();
-  int nwg = ncu < kMaxWg ? ncu : kMaxWg;
+  const int nwg = ncu < kMaxWg ? ncu : kMaxWg;
   a.nwg = nwg;
   a.rows_per_wg = (a.H + nwg - 1) / nwg;
-  const bool vec = (a.H % EPC == 0) && (a.I % EPC == 0) && (a.Is % EPC == 0) && aligned16(a.router) &&
-                   aligned16(a.eg) && aligned16(a.eu) && aligned16(a.ed) && aligned16(a.sg) && aligned16(a.su) &&
-                   aligned16(a.sd);
+  const bool vec = (a.H % EPC == 0) && (a.I % EPC == 0) && (a.Is % EPC == 0) && aligned16(a.x) &&
+                   aligned16(a.nw) && aligned16(a.router) && aligned16(a.eg) && aligned16(a.eu) && aligned16(a.ed) &&
+                   aligned16(a.sg) && aligned16(a.su) && aligned16(a.sd) && (a.wsg == nullptr || aligned16(a.wsg));
   const size_t lds = lds_bytes(kMaxB, a.H, a.E, a.I, a.Is, a.K, EPC, a.rows_per_wg);
   if (lds > size_t(max_lds_per_block()))
     return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: shape needs %zu bytes of LDS (> %d)", lds, max_lds_per_block());
   // Chunk counts per lane: the smallest instantiation that covers the rows.
   const int hc_need = (a.H + EPC * kWave - 1) / (EPC * kWave);
   const int ic_need = (max(a.I, a.Is) + EPC * kWave - 1) / (EPC * kWave);
-  void (*kern)(MoeArgs<T>) = nullptr;
-  if (vec && hc_need <= 4 && ic_need <= 1)
-    kern = &moe_decode_kernel<T, true, 4, 1>;
-  else if (vec)
-    kern = &moe_decode_kernel<T, true, kMaxHC, kMaxIC>;
-  else
-    kern = &moe_decode_kernel<T, false, kMaxHC, kMaxIC>;
-  static bool attr_set[3] = {false, false, false};
-  const int which = (vec && hc_need <= 4 && ic_need <= 1) ? 0 : (vec ? 1 : 2);
-  if (!attr_set[which]) {
+  const int which = (vec && hc_need <= 4 && ic_need <= 1) ? (batch == 1 ? 0 : 1) : (vec ? 2 : 3);
+  const bool el4 = a.E <= 4 * kWave;
+  void (*kern)(MoeArgs<T>) = which == 0   ? (el4 ? &moe_decode_kernel<T, true, 4, 1, 1, 4>
+                                                 : &moe_decode_kernel<T, true, 4, 1, 1, kMaxEL>)
+                             : which == 1 ? (el4 ? &moe_decode_kernel<T, true, 4, 1, kMaxB, 4>
+                                                 : &moe_decode_kernel<T, true, 4, 1, kMaxB, kMaxEL>)
+                             : which == 2 ? &moe_decode_kernel<T, true, kMaxHC, kMaxIC, kMaxB, kMaxEL>
+                                          : &moe_decode_kernel<T, false, kMaxHC, kMaxIC, kMaxB, kMaxEL>;
+  static bool attr_set[8] = {false, false, false, false, false, false, false, false};
+  const int slot = which * 2 + (el4 ? 1 : 0);
+  if (!attr_set[slot]) {
     MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     max_lds_per_block()));
-    attr_set[which] = true;
+    attr_set[slot] = true;
   }
   for (int b0 = 0; b0 < batch; b0 += kMaxB) {
     a.B = batch - b0 < kMaxB ? batch - b0 : kMaxB;
@@ -630,9 +841,7 @@ extern "C" size_t mkq_moe_decode_workspace_bytes(int batch, int hidden, int expe
   (void)batch;
   (void)hidden;
   if (experts <= 0 || intermediate <= 0 || shared_intermediate <= 0 || top_k <= 0) return 0;
-  const size_t data = sizeof(float) * (size_t(kMaxB) * experts + size_t(kMaxB) * top_k * intermediate +
-                                       size_t(kMaxB) * shared_intermediate);
-  return kOffData + data;
+  return ws_bytes(experts, intermediate, shared_intermediate, top_k);
 }
 
 extern "C" int mkq_moe_decode(int dtype, const void* x, const void* norm_weight, const void* router_weight,
@@ -652,39 +861,39 @@ extern "C" int mkq_moe_decode(int dtype, const void* x, const void* norm_weight,
                                                                               shared_intermediate, top_k),
               "moe_decode: workspace too small");
   MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "moe_decode: workspace must be 256-byte aligned");
-  if (experts > 1024 || top_k > 64)
-    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: experts <= 1024 and top_k <= 64 are supported");
-  const int maxh = 8 * kWave * kMaxHC / (dtype == MKQ_DTYPE_F32 ? 2 : 1);
-  const int maxi = 8 * kWave * kMaxIC / (dtype == MKQ_DTYPE_F32 ? 2 : 1);
+  if (experts > kMaxEL * kWave || top_k > 64)
+    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: experts <= %d and top_k <= 64 are supported", kMaxEL * kWave);
+  const int epc = dtype == MKQ_DTYPE_F32 ? 4 : 8;
+  const int maxh = epc * kWave * kMaxHC, maxi = epc * kWave * kMaxIC;
   if (hidden > maxh || intermediate > maxi || shared_intermediate > maxi)
     return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: hidden <= %d and intermediate <= %d are supported", maxh, maxi);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-#define MKQ_MOE_CASE(CODE, TYPE)                                                                                   \
-  case CODE: {                                                                                                     \
-    MoeArgs<TYPE> a{};                                                                                             \
-    a.x = static_cast<const TYPE*>(x);                                                                             \
-    a.nw = static_cast<const TYPE*>(norm_weight);                                                                  \
-    a.router = static_cast<const TYPE*>(router_weight);                                                            \
-    a.eg = static_cast<const TYPE*>(expert_gate);                                                                  \
-    a.eu = static_cast<const TYPE*>(expert_up);                                                                    \
-    a.ed = static_cast<const TYPE*>(expert_down);                                                                  \
-    a.sg = static_cast<const TYPE*>(shared_gate);                                                                  \
-    a.su = static_cast<const TYPE*>(shared_up);                                                                    \
-    a.sd = static_cast<const TYPE*>(shared_down);                                                                  \
-    a.wsg = static_cast<const TYPE*>(shared_expert_gate);                                                          \
-    a.out = static_cast<TYPE*>(out);                                                                               \
-    a.idx = indices;                                                                                               \
-    a.wts = weights;                                                                                               \
-    a.ws = static_cast<unsigned char*>(workspace);                                                                 \
-    a.H = hidden;                                                                                                  \
-    a.E = experts;                                                                                                 \
-    a.I = intermediate;                                                                                            \
-    a.Is = shared_intermediate;                                                                                    \
-    a.K = top_k;                                                                                                   \
-    a.eps = eps;                                                                                                   \
-    a.add_residual = add_residual;                                                                                 \
-    return launch<TYPE>(a, batch, s);                                                                              \
+#define MKQ_MOE_CASE(CODE, TYPE)                                 \
+  case CODE: {                                                   \
+    MoeArgs<TYPE> a{};                                           \
+    a.x = static_cast<const TYPE*>(x);                           \
+    a.nw = static_cast<const TYPE*>(norm_weight);                \
+    a.router = static_cast<const TYPE*>(router_weight);          \
+    a.eg = static_cast<const TYPE*>(expert_gate);                \
+    a.eu = static_cast<const TYPE*>(expert_up);                  \
+    a.ed = static_cast<const TYPE*>(expert_down);                \
+    a.sg = static_cast<const TYPE*>(shared_gate);                \
+    a.su = static_cast<const TYPE*>(shared_up);                  \
+    a.sd = static_cast<const TYPE*>(shared_down);                \
+    a.wsg = static_cast<const TYPE*>(shared_expert_gate);        \
+    a.out = static_cast<TYPE*>(out);                             \
+    a.idx = indices;                                             \
+    a.wts = weights;                                             \
+    a.ws = static_cast<unsigned char*>(workspace);               \
+    a.H = hidden;                                                \
+    a.E = experts;                                               \
+    a.I = intermediate;                                          \
+    a.Is = shared_intermediate;                                  \
+    a.K = top_k;                                                 \
+    a.eps = eps;                                                 \
+    a.add_residual = add_residual;                               \
+    return launch<TYPE>(a, batch, s);                            \
   }
     MKQ_MOE_CASE(MKQ_DTYPE_BF16, bf16_t)
     MKQ_MOE_CASE(MKQ_DTYPE_F16, f16_t)
