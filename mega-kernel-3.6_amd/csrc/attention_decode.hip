@@ -4,22 +4,29 @@
 // out[b, qh] = softmax(q[b,qh] . K[b,:,kvh]^T * scale) V[b,:,kvh],  kvh = qh / G
 // (reference.py:117-145; replaces attention_decode.cu:33-218).
 //
-// Work split: workgroup = (token chunk, kv head [, group of 16 q heads], batch
-// row); its 4 waves take 32-token tiles of the chunk in turn.  Per tile a wave
-//   * loads the K tile straight into MFMA A-operand registers (16 tokens x 32
-//     dims per v_mfma_f32_16x16x32, 16 bytes per lane) and computes S^T = K Q^T
-//     for all q heads of the group at once -- the G (=6) q heads that share a
-//     kv head reuse one read of K and V;
-//   * stages the V tile in wave-private LDS (row stride padded so the
-//     transposed 16-bit reads below are bank-conflict free);
+// Work split.  A "unit" is (batch row, kv head, group of <= 16 q heads that
+// share the kv head).  The token axis of each unit is cut into chunks; a
+// workgroup owns one (chunk, unit) and its 4 waves take the chunk's 16-token
+// tiles in turn, so at any moment the workgroup streams 64 adjacent tokens.
+// Workgroups of the same chunk for consecutive units are adjacent in launch
+// order, so the kv heads stored side by side in one token row are read
+// together.  Per tile a wave
+//   * holds the K tile in MFMA A-operand registers (16 tokens x 32 dims per
+//     v_mfma_f32_16x16x32, 16 bytes per lane) and computes S^T = K Q^T for all
+//     q heads of the group at once -- the G q heads of a kv head reuse one read
+//     of K and V;
 //   * runs an online softmax in the base-2 domain; the probabilities stay in
-//     registers in exactly the token order the PV product needs as its B
-//     operand (the S^T output of lane l covers tokens 4*(l/16)+i of each
-//     16-token half, which is the K-group of lane l in the PV MFMA);
-//   * accumulates O^T = V^T P^T with 16 MFMAs per 32 tokens (A operand read
-//     transposed from LDS).
-// The 4 waves merge in LDS; each workgroup writes one partial (m, l, O) and a
-// small merge kernel combines the chunks with the log-sum-exp rule.
+//     the registers of the S^T result, whose layout (lane (head c, group g)
+//     holds tokens 4g..4g+3) is exactly the B operand of v_mfma_f32_16x16x16;
+//   * stages the V tile in wave-private LDS (row stride padded so the
+//     transposed 16-bit reads are bank-conflict free) and accumulates
+//     O^T = V^T P^T with one 16x16x16 MFMA per 16 output dims.
+// K and V loads go through buffer descriptors that cover exactly the chunk,
+// so the tail of a chunk reads zeros with no branch, and the next tile's K and
+// V are issued while the current tile is computed.  The 4 waves merge in LDS;
+// each workgroup writes one partial (m, l, O) per q head and a merge kernel
+// combines the chunks with the log-sum-exp rule (a single chunk writes the
+// output directly).
 //
 // HBM-bound: every K/V byte is read once (4*T*Hkv*D bytes per batch row).
 #include <math.h>
@@ -32,210 +39,206 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kTile = 32;   // tokens per wave iteration
+constexpr int kTT = 16;                  // tokens per wave tile
+constexpr int kWgTokens = kWaves * kTT;  // tokens per workgroup pass
 constexpr int kMaxD = 256;
-constexpr int kMaxSteps = kMaxD / 32;   // QK^T MFMA steps over head_dim
-constexpr int kMaxDTiles = kMaxD / 16;  // PV MFMA tiles over head_dim
-constexpr int kMaxVChunks = kTile * kMaxD / 8 / kWave;  // 16-byte V chunks per lane per tile
+constexpr int kMaxChunks = 1024;
+constexpr int kMergeThreads = 1024;
+constexpr int kMergeSlices = kMergeThreads / kWave;
+constexpr int kMergeBatch = 8;           // chunk loads in flight per merge thread
+constexpr uint32_t kFar = 0x80000000u;   // pushes an offset past any descriptor (all < 2^31 bytes)
 constexpr float kNegInf = -INFINITY;
 
 template <typename T>
 struct Mfma;
 template <>
 struct Mfma<bf16_t> {
-  typedef bf16x8 vec;
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+  typedef bf16x8 vec8;
+  typedef short vec4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x4 qk(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ short from_float(float f) { return short(f2bf_bits(f)); }
+  static __device__ __forceinline__ f32x4 pv(vec4 a, vec4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ short cvt(float f) { return short(f2bf_bits(f)); }
 };
 template <>
 struct Mfma<f16_t> {
-  typedef f16x8 vec;
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+  typedef f16x8 vec8;
+  typedef _Float16 vec4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x4 qk(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ _Float16 from_float(float f) { return _Float16(f); }
+  static __device__ __forceinline__ f32x4 pv(vec4 a, vec4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ _Float16 cvt(float f) { return _Float16(f); }
 };
 
-// LDS row stride (in 16-bit elements) of the staged V tile: D/2 dwords padded
-// to 2 mod 8 dwords, so the four token rows a transposed read touches land in
-// four disjoint groups of 8 banks.
-__host__ __device__ inline int v_stride(int d) {
-  const int dw = d / 2;
-  const int pad = ((2 - dw) % 8 + 8) % 8;
-  return 2 * (dw + pad);
-}
+// LDS row stride (16-bit elements) of a staged V tile: D/2 dwords padded to
+// 2 mod 8 dwords, so the four token rows 4g+j (g = 0..3) that one transposed
+// read touches start 8 banks apart and cover 32 distinct banks.
+constexpr __host__ __device__ int v_stride(int d) { return 2 * (d / 2 + ((2 - d / 2) % 8 + 8) % 8); }
 
-__host__ __device__ inline size_t chunk_lds_bytes(int d) {
-  const size_t stage = size_t(kWaves) * kTile * v_stride(d) * 2;
-  const size_t merge = size_t(kWaves) * (32 + 16 * size_t(d)) * 4;
+// Row stride (floats) of a wave's O block in the merge area.
+__host__ __device__ inline int o_stride(int d) { return d + 4; }
+
+__host__ __device__ inline size_t merge_floats(int d, int heads) { return size_t(32) + size_t(heads) * o_stride(d); }
+
+template <int DT>
+size_t chunk_lds_bytes(int d, int heads) {
+  const size_t stage = size_t(kWaves) * kTT * v_stride(DT) * 2;
+  const size_t merge = size_t(kWaves) * merge_floats(d, heads) * 4;
   return stage > merge ? stage : merge;
 }
 
-// grid: (nchunks, kv_heads * head_groups, batch); block 256.
-template <typename T>
-__global__ __launch_bounds__(kThreads) void attn_chunk_kernel(const T* __restrict__ q, const T* __restrict__ kc,
-                                                              const T* __restrict__ vc, float* __restrict__ part_o,
-                                                              float* __restrict__ part_m, float* __restrict__ part_l,
-                                                              int hq, int hkv, int d, int seq, int group, int ngroups,
-                                                              int nchunks, int chunk_tokens, float scale_log2) {
-  typedef typename Mfma<T>::vec V8;
+// grid: (nchunks * units); block 256.  blockIdx.x = chunk * units + unit.
+template <typename T, int DT>
+__global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
+    const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, float* __restrict__ part_o,
+    float* __restrict__ part_m, float* __restrict__ part_l, T* __restrict__ out, int hq, int hkv, int d, int seq,
+    int group, int ngroups, int units, int nch, int chunk_tokens, float scale_log2) {
+  typedef typename Mfma<T>::vec8 V8;
+  typedef typename Mfma<T>::vec4 V4;
+  constexpr int NS = DT / 32;               // QK^T MFMA steps over head_dim
+  constexpr int NDT = DT / 16;              // PV MFMA tiles over head_dim
+  constexpr int CPR = DT / 8;               // 16-byte chunks per staged token row
+  constexpr int VCH = kTT * CPR / kWave;    // V chunks per lane per tile
+  constexpr int VSTR = v_stride(DT);
+  static_assert(VCH >= 1 && kTT * CPR == VCH * kWave, "V tile must split evenly over the wave");
+
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int col = lane & 15, grp = lane >> 4;
-  const int c = blockIdx.x, b = blockIdx.z;
-  const int kvh = blockIdx.y / ngroups, hg = blockIdx.y % ngroups;
+  const int unit = blockIdx.x % units, c = blockIdx.x / units;
+  const int b = unit / (hkv * ngroups);
+  const int kvh = (unit / ngroups) % hkv, hg = unit % ngroups;
   const int heads_here = min(16, group - hg * 16);
   const int qh0 = kvh * group + hg * 16;
-  const int nsteps = (d + 31) / 32;
-  const int ndt = (d + 15) / 16;
-  const int vstr = v_stride(d);
-  const int cpr = d / 8;  // 16-byte chunks per token row
-  uint16_t* vt = reinterpret_cast<uint16_t*>(smem) + size_t(wave) * kTile * vstr;
+  const int t_begin = c * chunk_tokens;
+  const int len = min(seq - t_begin, chunk_tokens);
+  const uint32_t tsb = uint32_t(hkv) * d * sizeof(T);  // bytes between tokens
 
-  // Q^T as the B operand: lane (head col, k-group grp) holds dims 32s+8grp..+8.
-  V8 qop[kMaxSteps];
+  // Descriptors over this unit's K/V rows of the chunk; anything past the
+  // last row (tail tokens, the prefetch after the last tile) reads zero.
+  const size_t base = (size_t(b) * seq + t_begin) * hkv * d + size_t(kvh) * d;
+  const uint32_t bytes = (uint32_t(len) - 1) * tsb + uint32_t(d) * sizeof(T);
+  const rsrc_t kr = make_rsrc(kc + base, bytes);
+  const rsrc_t vr = make_rsrc(vc + base, bytes);
+
+  // Q^T as the B operand: lane (head col, k-group grp) holds dims 32s+8grp..+8;
+  // heads past the group read zero.
+  const rsrc_t qr = make_rsrc(q + (size_t(b) * hq + qh0) * d, uint32_t(heads_here * d * sizeof(T)));
+  V8 qop[NS];
+  uint32_t koff[NS];
 #pragma unroll
-  for (int s = 0; s < kMaxSteps; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int d0 = 32 * s + 8 * grp;
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (s < nsteps && col < heads_here && d0 < d)
-      v = *reinterpret_cast<const u32x4*>(q + (size_t(b) * hq + qh0 + col) * d + d0);
-    qop[s] = __builtin_bit_cast(V8, v);
+    koff[s] = d0 < d ? uint32_t(d0 * sizeof(T)) : kFar;
+    qop[s] = __builtin_bit_cast(V8, buf_load16(qr, uint32_t(col * d * sizeof(T)) + koff[s]));
   }
-
-  f32x4 oacc[kMaxDTiles];
+  // V chunk i of a tile: token row qi / CPR, dims 8 * (qi % CPR), qi = lane + 64 i.
+  uint32_t voff[VCH];
 #pragma unroll
-  for (int n = 0; n < kMaxDTiles; ++n) oacc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < VCH; ++i) {
+    const int qi = lane + kWave * i;
+    const int row = qi / CPR, dc = qi % CPR;
+    voff[i] = uint32_t(row) * tsb + (dc * 8 < d ? uint32_t(dc * 16) : kFar);
+  }
+  uint16_t* vt = reinterpret_cast<uint16_t*>(smem) + size_t(wave) * kTT * VSTR;
+
+  f32x4 oacc[NDT];
+#pragma unroll
+  for (int n = 0; n < NDT; ++n) oacc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegInf, l_run = 0.f;
 
-  const int t_begin = c * chunk_tokens;
-  const int t_end = min(seq, t_begin + chunk_tokens);
-  const size_t tok_stride = size_t(hkv) * d;
-  const T* kb = kc + (size_t(b) * seq * hkv + kvh) * d;
-  const T* vb = vc + (size_t(b) * seq * hkv + kvh) * d;
+  u32x4 kreg[NS], vreg[VCH];
+  int t0 = wave * kTT;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) kreg[s] = buf_load16<kAuxStream>(kr, uint32_t(t0 + col) * tsb + koff[s]);
+#pragma unroll
+  for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, uint32_t(t0) * tsb + voff[i]);
 
-  for (int t0 = t_begin + wave * kTile; t0 < t_end; t0 += kWaves * kTile) {
-    // K tile -> A operands (token = 16*hh + col, dims 32s + 8grp).
-    V8 kop[2][kMaxSteps];
+  const int ntiles = len > t0 ? (len - t0 + kWgTokens - 1) / kWgTokens : 0;
+  for (int it = 0; it < ntiles; ++it, t0 += kWgTokens) {
+    // S^T = K Q^T: sacc[i] = score(token t0 + 4grp + i, head col).
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int tok = t0 + 16 * hh + col;
+    for (int s = 0; s < NS; ++s) sacc = Mfma<T>::qk(__builtin_bit_cast(V8, kreg[s]), qop[s], sacc);
+    const uint32_t next = uint32_t(t0 + kWgTokens) * tsb;
 #pragma unroll
-      for (int s = 0; s < kMaxSteps; ++s) {
-        const int d0 = 32 * s + 8 * grp;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (s < nsteps && tok < t_end && d0 < d)
-          v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + size_t(tok) * tok_stride + d0));
-        kop[hh][s] = __builtin_bit_cast(V8, v);
-      }
-    }
-    // V tile -> registers (coalesced 16-byte chunks; invalid tokens read as 0).
-    u32x4 vreg[kMaxVChunks];
+    for (int s = 0; s < NS; ++s) kreg[s] = buf_load16<kAuxStream>(kr, next + uint32_t(col) * tsb + koff[s]);
+
+    // Online softmax (base 2); m is kept equal across the 4 lanes of a head.
+    float sv[4];
 #pragma unroll
-    for (int i = 0; i < kMaxVChunks; ++i) {
-      const int qi = lane + kWave * i;
-      vreg[i] = u32x4{0u, 0u, 0u, 0u};
-      if (qi < kTile * cpr) {
-        const int row = qi / cpr, dc = qi % cpr;
-        const int tok = t0 + row;
-        if (tok < t_end)
-          vreg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + size_t(tok) * tok_stride + dc * 8));
-      }
-    }
-    // S^T = K Q^T: sacc[hh][i] = score(token t0+16hh+4grp+i, head col).
-    f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int s = 0; s < kMaxSteps; ++s) {
-      if (s < nsteps) {
-        sacc[0] = Mfma<T>::mma(kop[0][s], qop[s], sacc[0]);
-        sacc[1] = Mfma<T>::mma(kop[1][s], qop[s], sacc[1]);
-      }
-    }
-    // Stage V in LDS (two 8-byte stores per chunk: the padded stride is 8-byte aligned).
-#pragma unroll
-    for (int i = 0; i < kMaxVChunks; ++i) {
-      const int qi = lane + kWave * i;
-      if (qi < kTile * cpr) {
-        const int row = qi / cpr, dc = qi % cpr;
-        uint2* dst = reinterpret_cast<uint2*>(vt + row * vstr + dc * 8);
-        dst[0] = make_uint2(vreg[i].x, vreg[i].y);
-        dst[1] = make_uint2(vreg[i].z, vreg[i].w);
-      }
-    }
-    // Online softmax (base 2).  Element j of this lane's 8 scores is token
-    // tau(j) = (j < 4 ? 4grp + j : 16 + 4grp + j - 4) of the tile.
-    float sv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int hh = j >> 2, i = j & 3;
-      const int tok = t0 + 16 * hh + 4 * grp + i;
-      sv[j] = tok < t_end ? sacc[hh][i] * scale_log2 : kNegInf;
-    }
-    float mx = sv[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, sv[j]);
+    for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * grp + i < len ? sacc[i] * scale_log2 : kNegInf;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = fmaxf(mx, xor_lane(mx, 16));
     mx = fmaxf(mx, xor_lane(mx, 32));
     const float m_new = fmaxf(m_run, mx);
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    V8 pop;
+    V4 pop;
     float psum = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float p = __builtin_amdgcn_exp2f(sv[j] - m_new);
+    for (int i = 0; i < 4; ++i) {
+      const float p = __builtin_amdgcn_exp2f(sv[i] - m_new);
       psum += p;
-      pop[j] = Mfma<T>::from_float(p);
+      pop[i] = Mfma<T>::cvt(p);
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    // O^T = V^T P^T, A operand read transposed from LDS: dim 16n + col, tokens tau(j).
+
+    // Stage V (two 8-byte stores per chunk: the padded stride is 8-byte aligned),
+    // then prefetch the next tile's V into the freed registers.
 #pragma unroll
-    for (int n = 0; n < kMaxDTiles; ++n) {
-      if (n < ndt) {
-        const int dim = 16 * n + col;
-        union {
-          V8 v;
-          uint16_t u[8];
-        } va;
+    for (int i = 0; i < VCH; ++i) {
+      const int qi = lane + kWave * i;
+      uint2* dst = reinterpret_cast<uint2*>(vt + (qi / CPR) * VSTR + (qi % CPR) * 8);
+      dst[0] = make_uint2(vreg[i].x, vreg[i].y);
+      dst[1] = make_uint2(vreg[i].z, vreg[i].w);
+    }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int tok = (j < 4 ? 4 * grp + j : 16 + 4 * grp + (j - 4));
-          va.u[j] = vt[tok * vstr + dim];
-        }
-        oacc[n] = Mfma<T>::mma(va.v, pop, oacc[n] * alpha);
-      }
+    for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, next + voff[i]);
+
+    // O^T += V^T P^T: A operand = V[tokens 4grp..4grp+3][dim 16n + col] read transposed.
+#pragma unroll
+    for (int n = 0; n < NDT; ++n) {
+      union {
+        V4 v;
+        uint16_t u[4];
+      } va;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) va.u[j] = vt[(4 * grp + j) * VSTR + 16 * n + col];
+      oacc[n] = Mfma<T>::pv(va.v, pop, oacc[n] * alpha);
     }
   }
 
-  // Per-head l over the 4 lane groups (m is already uniform across them).
+  // Per-head l over the 4 lane groups (m is already equal across them).
   l_run += xor_lane(l_run, 16);
   l_run += xor_lane(l_run, 32);
 
-  __syncthreads();  // V staging area becomes the merge area
-  float* mw = reinterpret_cast<float*>(smem) + size_t(wave) * (32 + 16 * d);
-  float* lw = mw + 16;
-  float* ow = mw + 32;  // [16 heads][d]
-  if (grp == 0) {
+  __syncthreads();  // the V staging area becomes the merge area
+  const int ostr = o_stride(d);
+  const size_t wstride = merge_floats(d, min(16, group));
+  float* mw = reinterpret_cast<float*>(smem) + size_t(wave) * wstride;
+  if (grp == 0 && col < heads_here) {
     mw[col] = m_run;
-    lw[col] = l_run;
+    mw[16 + col] = l_run;
   }
+  if (col < heads_here) {
+    float* ow = mw + 32 + col * ostr;
 #pragma unroll
-  for (int n = 0; n < kMaxDTiles; ++n) {
-    if (n < ndt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int dim = 16 * n + 4 * grp + i;
-        if (dim < d) ow[col * d + dim] = oacc[n][i];
-      }
+    for (int n = 0; n < NDT; ++n) {
+      const int dim = 16 * n + 4 * grp;  // d % 8 == 0: all four dims valid or none
+      if (dim < d) *reinterpret_cast<f32x4*>(ow + dim) = oacc[n];
     }
   }
   __syncthreads();
   const float* m0 = reinterpret_cast<const float*>(smem);
-  const size_t wstride = 32 + 16 * size_t(d);
   for (int idx = threadIdx.x; idx < heads_here * d; idx += kThreads) {
-    const int hd = idx / d, dim = idx % d;
+    const int hd = idx / d, dim = idx - hd * d;
     float M = kNegInf;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m0[w * wstride + hd]);
@@ -244,62 +247,84 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(const T* __restric
     for (int w = 0; w < kWaves; ++w) {
       const float mwv = m0[w * wstride + hd];
       const float f = mwv == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mwv - M);
-      o += f * m0[w * wstride + 32 + hd * d + dim];
+      o += f * m0[w * wstride + 32 + hd * ostr + dim];
       L += f * m0[w * wstride + 16 + hd];
     }
-    const size_t pi = (size_t(b) * hq + qh0 + hd) * nchunks + c;
-    part_o[pi * d + dim] = o;
-    if (dim == 0) {
-      part_m[pi] = M;
-      part_l[pi] = L;
+    const size_t bq = size_t(b) * hq + qh0 + hd;
+    if (nch == 1) {
+      out[bq * d + dim] = from_f<T>(o / L);
+    } else {
+      const size_t pi = bq * nch + c;
+      part_o[pi * d + dim] = o;
+      if (dim == 0) {
+        part_m[pi] = M;
+        part_l[pi] = L;
+      }
     }
   }
 }
 
-// grid: (batch*q_heads, ceil(d/64)); block 256 = 64 dims x 4 chunk slices.
+// grid: (batch * q_heads, ceil(d / 64)); block 1024 = 64 dims x 16 chunk slices.
+// The first batch of partial-O loads is issued before the chunk weights are
+// computed, so both latencies overlap.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __restrict__ part_o,
-                                                              const float* __restrict__ part_m,
-                                                              const float* __restrict__ part_l, T* __restrict__ out,
-                                                              int d, int nchunks) {
-  __shared__ float red[kThreads];
-  __shared__ float bcast[2];
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict__ part_o,
+                                                                   const float* __restrict__ part_m,
+                                                                   const float* __restrict__ part_l,
+                                                                   T* __restrict__ out, int d, int nch) {
+  __shared__ float wgt[kMaxChunks];
+  __shared__ float red[kMergeSlices][kWave];
+  __shared__ float rw[2][kMergeSlices];
   const int bq = blockIdx.x;
-  const int tid = threadIdx.x, dl = tid & 63, cs = tid >> 6;
-  const int dim = blockIdx.y * 64 + dl;
-  const float* pm = part_m + size_t(bq) * nchunks;
-  const float* pl = part_l + size_t(bq) * nchunks;
+  const int tid = threadIdx.x, dl = tid % kWave, sl = tid / kWave;
+  const int dim = blockIdx.y * kWave + dl;
+  const rsrc_t por = make_rsrc(part_o + size_t(bq) * nch * d, uint32_t(size_t(nch) * d * 4));
+  const uint32_t doff = dim < d ? uint32_t(dim) * 4 : kFar;
+  float pv[kMergeBatch];
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; ++k) pv[k] = buf_loadf(por, uint32_t(sl + kMergeSlices * k) * d * 4 + doff);
 
+  const float* pm = part_m + size_t(bq) * nch;
+  const float* pl = part_l + size_t(bq) * nch;
   float M = kNegInf;
-  for (int c = tid; c < nchunks; c += kThreads) M = fmaxf(M, pm[c]);
+  for (int c = tid; c < nch; c += kMergeThreads) M = fmaxf(M, pm[c]);
   M = wave_max(M);
-  if ((tid & 63) == 0) red[tid >> 6] = M;
+  if (dl == 0) rw[0][sl] = M;
   __syncthreads();
-  if (tid == 0) {
-    float mm = red[0];
-    for (int w = 1; w < kWaves; ++w) mm = fmaxf(mm, red[w]);
-    bcast[0] = mm;
-  }
-  __syncthreads();
-  M = bcast[0];
+  M = rw[0][0];
+#pragma unroll
+  for (int s = 1; s < kMergeSlices; ++s) M = fmaxf(M, rw[0][s]);
   float L = 0.f;
-  for (int c = tid; c < nchunks; c += kThreads) L += pl[c] * __builtin_amdgcn_exp2f(pm[c] - M);
+  for (int c = tid; c < nch; c += kMergeThreads) {
+    const float mc = pm[c];
+    const float w = mc == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mc - M);
+    wgt[c] = w;
+    L += w * pl[c];
+  }
   L = wave_sum(L);
+  if (dl == 0) rw[1][sl] = L;
   __syncthreads();
-  if ((tid & 63) == 0) red[tid >> 6] = L;
-  __syncthreads();
-  if (tid == 0) bcast[1] = red[0] + red[1] + red[2] + red[3];
+  L = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMergeSlices; ++s) L += rw[1][s];
 
+  // Chunks past nch loaded zero; their weight index is clamped to a real one.
   float o = 0.f;
-  if (dim < d)
-    for (int c = cs; c < nchunks; c += kWaves)
-      o += part_o[(size_t(bq) * nchunks + c) * d + dim] * __builtin_amdgcn_exp2f(pm[c] - M);
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; ++k) o += wgt[min(sl + kMergeSlices * k, nch - 1)] * pv[k];
+  for (int c0 = kMergeSlices * kMergeBatch; c0 < nch; c0 += kMergeSlices * kMergeBatch) {
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) pv[k] = buf_loadf(por, uint32_t(c0 + sl + kMergeSlices * k) * d * 4 + doff);
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) o += wgt[min(c0 + sl + kMergeSlices * k, nch - 1)] * pv[k];
+  }
+  red[sl][dl] = o;
   __syncthreads();
-  red[tid] = o;
-  __syncthreads();
-  if (cs == 0 && dim < d) {
-    const float s = red[dl] + red[64 + dl] + red[128 + dl] + red[192 + dl];
-    out[size_t(bq) * d + dim] = from_f<T>(s / bcast[1]);
+  if (sl == 0 && dim < d) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMergeSlices; ++k) s += red[k][dl];
+    out[size_t(bq) * d + dim] = from_f<T>(s / L);
   }
 }
 
@@ -356,46 +381,83 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(const T* __restr
   }
 }
 
-int num_chunks(int batch, int hkv, int ngroups, int seq) {
-  const int max_chunks = (seq + kWaves * kTile - 1) / (kWaves * kTile);  // >= one tile per wave
-  const int want = (2 * cu_count() + batch * hkv * ngroups - 1) / (batch * hkv * ngroups);
-  int n = want < max_chunks ? want : max_chunks;
-  return n < 1 ? 1 : n;
+// Chunk geometry: about two workgroups per CU over all units, at least one
+// tile per wave, and every chunk's byte range addressable with 31-bit offsets
+// (including the prefetch one pass past its end).
+struct Chunking {
+  int nch;
+  int chunk_tokens;
+};
+
+int max_chunks(int seq) {
+  const int m = (seq + kWgTokens - 1) / kWgTokens;
+  return m < kMaxChunks ? m : kMaxChunks;
 }
 
-size_t fast_ws_floats(int batch, int hq, int d, int seq) {
-  const int max_chunks = (seq + kWaves * kTile - 1) / (kWaves * kTile);
-  return size_t(batch) * hq * max_chunks * (size_t(d) + 2);
+int plan_chunks(int units, int hkv, int d, int seq, size_t elt, Chunking* out) {
+  int nch = (2 * cu_count() + units - 1) / units;
+  const int cap = (seq + kWgTokens - 1) / kWgTokens;
+  nch = nch < cap ? nch : cap;
+  nch = nch < 1 ? 1 : nch;
+  int ct = (seq + nch - 1) / nch;
+  ct = (ct + kWgTokens - 1) / kWgTokens * kWgTokens;
+  const size_t tsb = size_t(hkv) * d * elt;
+  const size_t limit_tokens = (size_t(1) << 31) / tsb;
+  if (size_t(ct) + 2 * kWgTokens > limit_tokens) {
+    if (limit_tokens < size_t(3 * kWgTokens))
+      return set_error(MKQ_ERR_UNSUPPORTED, "full_attention_decode: token row of %zu bytes is too large", tsb);
+    ct = int((limit_tokens - 2 * kWgTokens) / kWgTokens * kWgTokens);
+  }
+  nch = (seq + ct - 1) / ct;
+  if (nch > kMaxChunks)
+    return set_error(MKQ_ERR_UNSUPPORTED, "full_attention_decode: seq_len %d needs %d chunks (max %d)", seq, nch,
+                     kMaxChunks);
+  out->nch = nch;
+  out->chunk_tokens = ct;
+  return MKQ_OK;
 }
 
-template <typename T>
+size_t fast_ws_floats(int batch, int hq, int d, int seq) { return size_t(batch) * hq * max_chunks(seq) * (size_t(d) + 2); }
+
+template <typename T, int DT>
 int launch_fast(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
                 float scale, float* ws, hipStream_t stream) {
   const int group = hq / hkv;
   const int ngroups = (group + 15) / 16;
-  const int nchunks = num_chunks(batch, hkv, ngroups, seq);
-  int chunk_tokens = (seq + nchunks - 1) / nchunks;
-  chunk_tokens = (chunk_tokens + kTile - 1) / kTile * kTile;
-  const int nch = (seq + chunk_tokens - 1) / chunk_tokens;
-  const size_t lds = chunk_lds_bytes(d);
+  const int units = batch * hkv * ngroups;
+  Chunking ch;
+  const int rc = plan_chunks(units, hkv, d, seq, sizeof(T), &ch);
+  if (rc != MKQ_OK) return rc;
+  const size_t lds = chunk_lds_bytes<DT>(d, group < 16 ? group : 16);
   static bool attr_set = false;
   if (!attr_set) {
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(chunk_lds_bytes(kMaxD))));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    int(chunk_lds_bytes<DT>(DT, 16))));
     attr_set = true;
   }
+  MKQ_REQUIRE(size_t(ch.nch) * units < (size_t(1) << 31), "full_attention_decode: grid too large");
   float* part_o = ws;
-  float* part_m = part_o + size_t(batch) * hq * nch * d;
-  float* part_l = part_m + size_t(batch) * hq * nch;
-  dim3 g1(nch, hkv * ngroups, batch);
-  attn_chunk_kernel<T><<<g1, kThreads, lds, stream>>>(static_cast<const T*>(q), static_cast<const T*>(k),
-                                                      static_cast<const T*>(v), part_o, part_m, part_l, hq, hkv, d,
-                                                      seq, group, ngroups, nch, chunk_tokens, scale * kLog2e);
+  float* part_m = part_o + size_t(batch) * hq * ch.nch * d;
+  float* part_l = part_m + size_t(batch) * hq * ch.nch;
+  attn_chunk_kernel<T, DT><<<dim3(ch.nch * units), kThreads, lds, stream>>>(
+      static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), part_o, part_m, part_l,
+      static_cast<T*>(out), hq, hkv, d, seq, group, ngroups, units, ch.nch, ch.chunk_tokens, scale * kLog2e);
   MKQ_LAUNCH_CHECK("attn_chunk_kernel");
-  dim3 g2(batch * hq, (d + 63) / 64);
-  attn_merge_kernel<T><<<g2, kThreads, 0, stream>>>(part_o, part_m, part_l, static_cast<T*>(out), d, nch);
-  MKQ_LAUNCH_CHECK("attn_merge_kernel");
+  if (ch.nch > 1) {
+    dim3 g2(batch * hq, (d + kWave - 1) / kWave);
+    attn_merge_kernel<T><<<g2, kMergeThreads, 0, stream>>>(part_o, part_m, part_l, static_cast<T*>(out), d, ch.nch);
+    MKQ_LAUNCH_CHECK("attn_merge_kernel");
+  }
   return MKQ_OK;
+}
+
+template <typename T>
+int launch_fast_d(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
+                  float scale, float* ws, hipStream_t stream) {
+  if (d <= 64) return launch_fast<T, 64>(q, k, v, out, batch, hq, hkv, d, seq, scale, ws, stream);
+  if (d <= 128) return launch_fast<T, 128>(q, k, v, out, batch, hq, hkv, d, seq, scale, ws, stream);
+  return launch_fast<T, 256>(q, k, v, out, batch, hq, hkv, d, seq, scale, ws, stream);
 }
 
 template <typename T>
@@ -438,13 +500,13 @@ extern "C" int mkq_full_attention_decode(int dtype, const void* q, const void* k
   const bool fast_ok = (head_dim % 8 == 0) && aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
   switch (dtype) {
     case MKQ_DTYPE_BF16:
-      return fast_ok ? launch_fast<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                           scale, ws, s)
+      return fast_ok ? launch_fast_d<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
+                                             scale, ws, s)
                      : launch_generic<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                               scale, ws, s);
     case MKQ_DTYPE_F16:
-      return fast_ok ? launch_fast<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                          scale, ws, s)
+      return fast_ok ? launch_fast_d<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
+                                            scale, ws, s)
                      : launch_generic<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                              scale, ws, s);
     case MKQ_DTYPE_F32:

@@ -92,10 +92,14 @@ def bf16_round(a) -> np.ndarray:
 # ---------------------------------------------------------------------------
 
 def rms_norm(x, weight, eps: float = 1e-6) -> np.ndarray:
-    """``x * rsqrt(mean(x^2) + eps) * weight`` in FP32 (reference.py:10-13).
+    """``(x * rsqrt(mean(x^2) + eps)) * weight`` in FP32 (reference.py:10-13).
 
-    The reference ends with ``.to(x.dtype)``; for the FP32 inputs the oracle is
-    run on that cast is the identity, so the result stays FP32 here.
+    reference.py ends with ``.to(x.dtype)``, which rounds x_norm to bf16 for
+    bf16 inputs.  The CUDA kernels this path replaces keep x_norm in FP32
+    (persistent_moe_decode.cu:28-30, 280), and so do the HIP kernels, so the
+    oracle keeps it in FP32 too.  The difference is below the bf16 output
+    tolerance; the reference's own GPU tests compare its FP32-x_norm kernel with
+    reference.py the same way (tests/test_cuda_ops.py:25-36).
     """
     xf = as_f32(x)
     var = np.mean(xf * xf, axis=-1, keepdims=True, dtype=np.float32)

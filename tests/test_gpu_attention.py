@@ -47,6 +47,10 @@ def test_attention_config4_128k():
     (1, 32, 1, 64, 300),     # group 32 -> two head groups
     (2, 8, 2, 40, 50),       # head_dim 40: 8-multiple, partial MFMA step
     (1, 4, 2, 20, 33),       # head_dim 20: generic path
+    (1, 12, 2, 96, 4500),    # head_dim 96 on the 128-wide kernel, several chunks
+    (2, 40, 2, 128, 2049),   # group 20 -> head groups of 16 and 4, batch 2
+    (1, 8, 8, 256, 16),      # exactly one tile
+    (1, 24, 4, 256, 65),     # one token past a workgroup pass
 ])
 def test_attention_odd_shapes(shape):
     b, hq, hkv, d, t = shape
