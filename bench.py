@@ -9,8 +9,10 @@ other batch sizes are under ``"ops"``.
 
 Timing method (reference benchmarks/bench_utils.py:17-56, plus a cache flush):
 inputs are resident in HBM; before every timed step a 1 GiB buffer is
-rewritten so that neither the 4 MB L2s nor the 256 MB MALL hold the op's
-working set; each step is bracketed by HIP events recorded on the stream the
+streamed through a reduction (``--flush read``, the default) so that neither
+the 4 MB L2s nor the 256 MB MALL hold the op's working set and no dirty lines
+are left to be written back during the op (``--flush write`` rewrites the
+buffer instead); each step is bracketed by HIP events recorded on the stream the
 kernels run on (torch's current stream); the median over K steps is reported.
 Algorithmic bytes count every weight/KV/state byte that must be read once plus
 inputs and outputs.
@@ -71,9 +73,20 @@ def linear_bytes(batch, k_heads, v_heads, dk, dv, elt=2):
 # ---------------------------------------------------------------------------
 
 class Timer:
-    def __init__(self, torch, flush_bytes=1 << 30):
+    def __init__(self, torch, flush_bytes=1 << 30, mode="read"):
         self.torch = torch
-        self.flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device="cuda")
+        self.mode = mode
+        self.flush = torch.zeros(flush_bytes // 4, dtype=torch.float32, device="cuda")
+
+    def evict(self):
+        # "read" streams the buffer through a reduction: caches end up holding
+        # clean lines of the flush buffer.  "write" rewrites it, which leaves
+        # up to the 256 MB memory-side cache dirty; the timed op then pays for
+        # those write-backs.
+        if self.mode == "read":
+            self.flush.sum()
+        elif self.mode == "write":
+            self.flush.add_(1.0)
 
     def run(self, fn, steps: int, warmup: int, cold: bool = True):
         torch = self.torch
@@ -85,7 +98,7 @@ class Timer:
         t0 = time.perf_counter()
         for i in range(steps):
             if cold:
-                self.flush.add_(1.0)
+                self.evict()
             starts[i].record()
             fn()
             ends[i].record()
@@ -147,7 +160,8 @@ def bench_dense(mk, inputs, timer, steps, warmup, batches):
         warm = timer.run(fn, steps, warmup, cold=False)
         cold["warm_median_us"] = warm["median_us"]
         out[f"dense_b{b}"] = cold
-        log(f"dense b={b}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s)")
+        log(f"dense b={b}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s), "
+            f"{cold['warm_median_us']:.2f} us warm")
         if b == 1:
             t = timer.run(lambda: mk.dense_ffn_decode(x, w, backend="torch"), steps, warmup, cold=True)
             out["dense_b1_torch_composite_same_gpu"] = {"median_us": t["median_us"]}
@@ -164,8 +178,10 @@ def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
         inp = inputs.make_attention(seq_len=t)
         fn = lambda: mk.full_attention_decode(inp)  # noqa: E731
         cold = with_bw(timer.run(fn, steps, warmup, cold=True), attn_bytes(1, 24, 4, 256, t))
+        cold["warm_median_us"] = timer.run(fn, steps, warmup, cold=False)["median_us"]
         out[f"attn_t{t}"] = cold
-        log(f"attention T={t}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s)")
+        log(f"attention T={t}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s), "
+            f"{cold['warm_median_us']:.2f} us warm")
         del inp
         torch.cuda.empty_cache()
     return out
@@ -177,8 +193,10 @@ def bench_linear(mk, inputs, timer, steps, warmup, batches):
         inp = inputs.make_gated_delta(batch=b)
         fn = lambda: mk.linear_attention_decode(inp)  # noqa: E731
         cold = with_bw(timer.run(fn, steps, warmup, cold=True), linear_bytes(b, 16, 32, 128, 128))
+        cold["warm_median_us"] = timer.run(fn, steps, warmup, cold=False)["median_us"]
         out[f"linear_b{b}"] = cold
-        log(f"linear b={b}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s)")
+        log(f"linear b={b}: {cold['median_us']:.2f} us cold ({cold['gbps']:.0f} GB/s), "
+            f"{cold['warm_median_us']:.2f} us warm")
     return out
 
 
@@ -241,6 +259,8 @@ def main(argv=None):
     ap.add_argument("--ops", default="moe,dense,attn,linear")
     ap.add_argument("--quick", action="store_true", help="batch 1 / 32K only")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
+    ap.add_argument("--flush", choices=("read", "write"), default="read",
+                    help="how the 1 GiB cache flush before each cold step touches its buffer")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -261,7 +281,7 @@ def main(argv=None):
     dev = torch.cuda.get_device_properties(0)
     log(f"device {dev.name} {getattr(dev, 'gcnArchName', '')} CUs={dev.multi_processor_count}")
 
-    timer = Timer(torch)
+    timer = Timer(torch, mode=args.flush)
     ops = set(args.ops.split(","))
     results = {}
     t_start = time.perf_counter()

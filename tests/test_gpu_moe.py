@@ -1,7 +1,8 @@
 """GPU parity: persistent MoE decode (one HIP launch) vs the CPU oracle.
 
-Task tolerances: top-k indices bit-exact; router weights and bf16 outputs
-atol 1e-2 / rtol 1e-2 against the oracle run on FP32 upcasts of the inputs.
+Task tolerances: top-k indices bit-exact; bf16 outputs atol 1e-2 / rtol 1e-2
+against the oracle run on FP32 upcasts of the inputs; router weights (FP32)
+atol 1e-5 / rtol 1e-4.
 """
 
 import numpy as np
@@ -36,7 +37,8 @@ def _check(x, w, k, backend="persistent", add_residual=True):
     assert out.shape == x.shape and out.dtype == x.dtype
     assert idx.dtype == torch.int64 and rw.dtype == torch.float32
     assert idx.cpu().tolist() == ref_idx.tolist()
-    assert_close_out(rw, ref_w)
+    # FP32 softmax over FP32 logits: only the summation order differs.
+    torch.testing.assert_close(rw.cpu(), torch.from_numpy(np.asarray(ref_w, dtype=np.float32)), atol=1e-5, rtol=1e-4)
     assert_close_out(out, ref)
     return out, idx, rw
 
