@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   static_assert(VCH >= 1 && kTT * CPR == VCH * kWave, "V tile must split evenly over the wave");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave, wave = wave_id();
   const int col = lane & 15, grp = lane >> 4;
   const int unit = blockIdx.x % units, c = blockIdx.x / units;
   const int b = unit / (hkv * ngroups);
@@ -159,6 +159,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   for (int s = 0; s < NS; ++s) kreg[s] = buf_load16<kAuxStream>(kr, uint32_t(t0 + col) * tsb + koff[s]);
 #pragma unroll
   for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, uint32_t(t0) * tsb + voff[i]);
+  pin_loads();
 
   const int ntiles = len > t0 ? (len - t0 + kWgTokens - 1) / kWgTokens : 0;
   for (int it = 0; it < ntiles; ++it, t0 += kWgTokens) {
@@ -169,6 +170,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const uint32_t next = uint32_t(t0 + kWgTokens) * tsb;
 #pragma unroll
     for (int s = 0; s < NS; ++s) kreg[s] = buf_load16<kAuxStream>(kr, next + uint32_t(col) * tsb + koff[s]);
+    pin_loads();
 
     // Online softmax (base 2); m is kept equal across the 4 lanes of a head.
     float sv[4];
@@ -201,6 +203,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     }
 #pragma unroll
     for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, next + voff[i]);
+    pin_loads();
 
     // O^T += V^T P^T: A operand = V[tokens 4grp..4grp+3][dim 16n + col] read transposed.
 #pragma unroll
@@ -283,6 +286,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
   float pv[kMergeBatch];
 #pragma unroll
   for (int k = 0; k < kMergeBatch; ++k) pv[k] = buf_loadf(por, uint32_t(sl + kMergeSlices * k) * d * 4 + doff);
+  pin_loads();
 
   const float* pm = part_m + size_t(bq) * nch;
   const float* pl = part_l + size_t(bq) * nch;

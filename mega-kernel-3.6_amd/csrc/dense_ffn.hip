@@ -88,7 +88,7 @@ template <typename T, int NB, bool VEC>
 __device__ void stage_xnorm(const T* __restrict__ x, const T* __restrict__ nw, int h, int hp, float eps,
                             float* lds_xn, float* lds_red) {
   constexpr int EPC = Epc<T>::value;
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
   float ss[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) ss[b] = 0.f;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void ffn_gateup_kernel(const T* __restric
   constexpr int EPC = Epc<T>::value;
   extern __shared__ float smem[];
   const int hp = round_up(h, EPC);
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave, wave = wave_id();
   const int last = hp / EPC - 1;
   const int rb = blockIdx.x * rows_per_wg;
   const int nr = min(rows_per_wg, inter - rb);
@@ -191,6 +191,7 @@ __global__ __launch_bounds__(kThreads) void ffn_gateup_kernel(const T* __restric
   };
   issue(wave, ca);
   issue(wave + kWaves, cb);
+  pin_loads();
 
   float* xn = smem;
   float* red = smem + NB * hp;
@@ -208,8 +209,10 @@ __global__ __launch_bounds__(kThreads) void ffn_gateup_kernel(const T* __restric
   for (int item = wave; item < nitems; item += 2 * kWaves) {
     finish(item, ca);
     issue(item + 2 * kWaves, ca);
+    pin_loads();
     finish(item + kWaves, cb);
     issue(item + 3 * kWaves, cb);
+    pin_loads();
   }
   __syncthreads();
   for (int t = threadIdx.x; t < nr * NB; t += kThreads) {
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
   const int qch = (nch + kQuarters - 1) / kQuarters;  // chunks per quarter (last one may be shorter)
   float* a = smem;
   float* part = smem + NB * ip;
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
   const int rb = blockIdx.x * rows_per_wg;
   const int nr = min(rows_per_wg, h - rb);
   const int nitems = nr * kQuarters;
@@ -258,6 +261,7 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
   // Weight loads of the first two items go out before act is staged.
   issue(wave, ca);
   issue(wave + kWaves, cb);
+  pin_loads();
 
   // act -> LDS: 16-byte buffer loads, kActUnroll per thread in flight (act
   // rows are 16-byte aligned: act_ld == inter and inter % EPC == 0 on the
@@ -265,14 +269,16 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
   if constexpr (VEC) {
     constexpr int kActUnroll = 16;
     const int q4 = ip / 4;
+    // One descriptor over all NB rows (a per-row descriptor would depend on the
+    // lane's row and force a readfirstlane loop around every load).
+    const rsrc_t ar = make_rsrc(act, uint32_t(NB - 1) * uint32_t(act_ld) * 4u + uint32_t(inter) * 4u);
     for (int f0 = tid; f0 < NB * q4; f0 += kActUnroll * kThreads) {
       u32x4 v[kActUnroll];
 #pragma unroll
       for (int r = 0; r < kActUnroll; ++r) {
         const int f = f0 + r * kThreads;
         const int b = f / q4, c4 = f % q4;
-        v[r] = buf_load16(make_rsrc(act + size_t(b) * act_ld, uint32_t(inter) * 4u),
-                          f < NB * q4 ? uint32_t(c4) * 16u : 0xFFFFFFF0u);
+        v[r] = buf_load16(ar, f < NB * q4 ? (uint32_t(b) * uint32_t(act_ld) + uint32_t(c4) * 4u) * 4u : 0xFFFFFFF0u);
       }
 #pragma unroll
       for (int r = 0; r < kActUnroll; ++r) {
@@ -302,8 +308,10 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
   for (int item = wave; item < nitems; item += 2 * kWaves) {
     finish(item, ca);
     issue(item + 2 * kWaves, ca);
+    pin_loads();
     finish(item + kWaves, cb);
     issue(item + 3 * kWaves, cb);
+    pin_loads();
   }
   __syncthreads();
   for (int t = tid; t < nr * NB; t += kThreads) {

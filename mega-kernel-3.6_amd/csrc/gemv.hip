@@ -23,7 +23,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x,
 #pragma unroll
     for (int b = 0; b < NB; ++b) xs[b * kp + i] = i < kdim ? to_f(x[size_t(b) * kdim + i]) : 0.f;
   __syncthreads();
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave, wave = wave_id();
   const int nch = kp / EPC;
   const int r0 = blockIdx.x * rows_per_wg, r1 = min(n, r0 + rows_per_wg);
   for (int r = r0 + wave; r < r1; r += kWaves) {

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
   __shared__ float ks[kMaxKeyDim];
   __shared__ float red[kWaves][kWave];
 
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave, wave = wave_id();
   const int j = blockIdx.x * kWave + lane;  // value column
   const int vh = blockIdx.y;
   const int b = blockIdx.z;

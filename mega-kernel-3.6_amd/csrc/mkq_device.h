@@ -14,6 +14,20 @@ namespace mkq {
 
 constexpr int kWave = 64;
 
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar)
+// value.  threadIdx.x / 64 is the same in every lane, but the compiler treats
+// it as divergent; buffer descriptors and row addresses derived from it would
+// then be built per lane and every buffer load wrapped in a readfirstlane
+// loop.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave); }
+
+// Keeps the loads issued above this point where they are.  The compiler sinks
+// a load to the block of its first use when nothing in between may write the
+// loaded memory -- across loops and barriers -- which turns an early prefetch
+// into a load waited on immediately.  An empty asm that clobbers memory is a
+// point no load may cross; it has no register operands, so it adds no wait.
+__device__ __forceinline__ void pin_loads() { asm volatile("" ::: "memory"); }
+
 // bfloat16 storage type (bit pattern).
 struct bf16_t {
   uint16_t bits;
@@ -204,6 +218,25 @@ __device__ __forceinline__ float wave_sum_u(float v) {
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Two independent wave sums, their DPP steps interleaved so that each step's
+// latency is hidden behind the other's; results wave-uniform.
+__device__ __forceinline__ void wave_sum2_u(float& a, float& b) {
+  a += dpp<0xB1>(a);
+  b += dpp<0xB1>(b);
+  a += dpp<0x4E>(a);
+  b += dpp<0x4E>(b);
+  a += dpp<0x124>(a);
+  b += dpp<0x124>(b);
+  a += dpp<0x128>(a);
+  b += dpp<0x128>(b);
+  a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x142, 0xA, 0xF, false));
+  b += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(b), 0x142, 0xA, 0xF, false));
+  a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x143, 0xC, 0xF, false));
+  b += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(b), 0x143, 0xC, 0xF, false));
+  a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 63));
+  b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), 63));
 }
 
 // (value, index) of the largest value over the wave, ties to the lower index;

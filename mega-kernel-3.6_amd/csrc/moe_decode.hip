@@ -156,20 +156,40 @@ __device__ __forceinline__ void load_row(const T* __restrict__ row, int n, bool 
 // multiple of EPC).  Branch-free: a chunk past the row was loaded as zeros,
 // so it is multiplied with the (finite) last chunk of the vector instead of
 // being skipped.
+// One accumulator per chunk keeps the FMA chains short (they run in
+// parallel); the chunk sums are added pairwise at the end.  The vector is read
+// as float4s: every LDS vector handed in here is 16-byte aligned, and
+// 16-byte reads keep the 32-byte lane stride to a 2-way bank conflict, where
+// the 8-byte pair reads the compiler otherwise emits serialise much further.
 template <typename T, int MAXC>
 __device__ __forceinline__ float dot_row(const u32x4 (&c)[MAXC], const float* __restrict__ v, int n, int lane) {
   constexpr int EPC = Epc<T>::value;
   const int last = (n + EPC - 1) / EPC - 1;
-  float s = 0.f;
+  float s[MAXC];
 #pragma unroll
   for (int j = 0; j < MAXC; ++j) {
     const int q = min(lane + kWave * j, last);
     float f[EPC];
     unpack(c[j], f, T{});
+    const float4* p = reinterpret_cast<const float4*>(v + q * EPC);
+    float vv[EPC];
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) s = fmaf(f[e], v[q * EPC + e], s);
+    for (int h = 0; h < EPC / 4; ++h) {
+      const float4 t = p[h];
+      vv[4 * h] = t.x;
+      vv[4 * h + 1] = t.y;
+      vv[4 * h + 2] = t.z;
+      vv[4 * h + 3] = t.w;
+    }
+    s[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) s[j] = fmaf(f[e], vv[e], s[j]);
   }
-  return s;
+#pragma unroll
+  for (int st = 1; st < MAXC; st *= 2)
+#pragma unroll
+    for (int j = 0; j + st < MAXC; j += 2 * st) s[j] += s[j + st];
+  return s[0];
 }
 
 // Gathers `pairs` pairs of tagged words (word 2p, 2p+1 of the array behind
@@ -222,7 +242,7 @@ template <typename T, bool VEC, int HC, int IC, int MB, int EL>
 __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   constexpr int EPC = Epc<T>::value;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = wave_id();
   const int wg = blockIdx.x, nwg = a.nwg;
   const int B = a.B, H = a.H, E = a.E, I = a.I, Is = a.Is, K = a.K;
   const int Hp = round_up(H, EPC), Ip = round_up(I, EPC), Isp = round_up(Is, EPC);
@@ -271,19 +291,33 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // one).  Loaded by every thread (no branch) after x, so the norm does not
   // wait for it; the tag is first used after the norm.
   const unsigned gen = __hip_atomic_load(w.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // One-row path: the residual of this wave's output row, fetched now; after
+  // the expert weights have streamed through, x is no longer in the L2.
+  float x_res = 0.f;
+  if constexpr (MB == 1) x_res = to_f(a.x[min(wg * a.rows_per_wg + wave, H - 1)]);
   const int e0 = wg + nwg * wave;  // first router row of this wave
   u32x4 rrow[HC];
   load_row<T, VEC, HC>(a.router + size_t(min(e0, E - 1)) * H, H, e0 < E, lane, rrow);
   const int s0 = wg + nwg * (kWaves - 1 - wave);  // first shared gate/up row of this wave
-  u32x4 sgr[HC], sur[HC];
-  load_row<T, VEC, HC>(a.sg + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sgr);
-  load_row<T, VEC, HC>(a.su + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sur);
-  // Shared-expert down row of this wave's first output row: independent of
-  // the routing, so it is fetched now, while HBM would otherwise idle.
   const int h0 = wg * a.rows_per_wg;
   const int nrows = max(0, min(a.rows_per_wg, H - h0));
-  u32x4 sdn[IC];
-  load_row<T, VEC, IC>(a.sd + size_t(min(h0 + wave, H - 1)) * Is, Is, wave < nrows, lane, sdn);
+  // Shared-expert gate/up rows and the shared down row of this wave's first
+  // output row are independent of the routing.  The multi-row path fetches
+  // them now; the one-row path only once its router logits are out, so that
+  // the router rows do not queue behind 6 MB of shared-expert rows.
+  u32x4 sgr[HC], sur[HC], sdn[IC];
+  auto issue_shared_gu = [&]() {
+    load_row<T, VEC, HC>(a.sg + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sgr);
+    load_row<T, VEC, HC>(a.su + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sur);
+  };
+  auto issue_shared_down = [&]() {
+    load_row<T, VEC, IC>(a.sd + size_t(min(h0 + wave, H - 1)) * Is, Is, wave < nrows, lane, sdn);
+  };
+  if constexpr (MB > 1) {
+    issue_shared_gu();
+    issue_shared_down();
+  }
+  pin_loads();
 
   if constexpr (MB > 1)
     for (int e = tid; e < E; e += kThreads) emask[e] = 0u;
@@ -314,10 +348,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
             unpack(xc[r], xf, T{});
             unpack(nc[r], nf, T{});
             float sq = 0.f;
+            float4* dst = reinterpret_cast<float4*>(xn + b * Hp + c * EPC);
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) {
-              sq = fmaf(xf[e], xf[e], sq);
-              xn[b * Hp + c * EPC + e] = xf[e] * nf[e];
+            for (int h = 0; h < EPC / 4; ++h) {
+#pragma unroll
+              for (int e = 4 * h; e < 4 * h + 4; ++e) sq = fmaf(xf[e], xf[e], sq);
+              dst[h] = make_float4(xf[4 * h] * nf[4 * h], xf[4 * h + 1] * nf[4 * h + 1], xf[4 * h + 2] * nf[4 * h + 2],
+                                   xf[4 * h + 3] * nf[4 * h + 3]);
             }
 #pragma unroll
             for (int bb = 0; bb < MB; ++bb) ss[bb] += bb == b ? sq : 0.f;
@@ -368,11 +405,19 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
 #pragma unroll
             for (int bb = 0; bb < MB; ++bb) ib = bb == b ? inv[bb] : ib;
             float dg = 0.f;
+            float4* xv = reinterpret_cast<float4*>(xn + b * Hp + c * EPC);
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) {
-              const float v = xn[b * Hp + c * EPC + e] * ib;
-              xn[b * Hp + c * EPC + e] = v;
-              dg = fmaf(v, gf[e], dg);
+            for (int h = 0; h < EPC / 4; ++h) {
+              float4 v = xv[h];
+              v.x *= ib;
+              v.y *= ib;
+              v.z *= ib;
+              v.w *= ib;
+              xv[h] = v;
+              dg = fmaf(v.x, gf[4 * h], dg);
+              dg = fmaf(v.y, gf[4 * h + 1], dg);
+              dg = fmaf(v.z, gf[4 * h + 2], dg);
+              dg = fmaf(v.w, gf[4 * h + 3], dg);
             }
 #pragma unroll
             for (int bb = 0; bb < MB; ++bb) gs[bb] += bb == b ? dg : 0.f;
@@ -417,20 +462,243 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         if (lane == 0) put_tagged(w.logits + size_t(b) * E + e, s, tag);
       }
   }
-  // Shared-expert gate/up of this wave's rows.
-  for (int s = s0, r = 0; s < Is; s += nwg * kWaves, ++r) {
-    if (r > 0) {
-      load_row<T, VEC, HC>(a.sg + size_t(s) * H, H, true, lane, sgr);
-      load_row<T, VEC, HC>(a.su + size_t(s) * H, H, true, lane, sur);
-    }
-#pragma unroll
-    for (int b = 0; b < MB; ++b)
-      if (b < B) {
-        const float g = wave_sum_u(dot_row<T, HC>(sgr, xn + b * Hp, H, lane));
-        const float u = wave_sum_u(dot_row<T, HC>(sur, xn + b * Hp, H, lane));
-        if (lane == 0) put_tagged(w.sact + size_t(b) * Is + s, silu(g) * u, tag);
+  // Shared-expert gate/up of this wave's rows.  The one-row path runs this
+  // after issuing its routed loads: the shared rows arrive behind the router
+  // row, and the routing must not wait for them.
+  auto publish_shared = [&]() {
+    for (int s = s0, r = 0; s < Is; s += nwg * kWaves, ++r) {
+      if (r > 0) {
+        load_row<T, VEC, HC>(a.sg + size_t(s) * H, H, true, lane, sgr);
+        load_row<T, VEC, HC>(a.su + size_t(s) * H, H, true, lane, sur);
       }
-  }
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+        if (b < B) {
+          const float g = wave_sum_u(dot_row<T, HC>(sgr, xn + b * Hp, H, lane));
+          const float u = wave_sum_u(dot_row<T, HC>(sur, xn + b * Hp, H, lane));
+          if (lane == 0) put_tagged(w.sact + size_t(b) * Is + s, silu(g) * u, tag);
+        }
+    }
+  };
+  if constexpr (MB > 1) publish_shared();
+
+  if constexpr (MB == 1) {
+    issue_shared_gu();
+    pin_loads();
+    // ---- phases 1-2, one batch row: every wave routes on its own ------------
+    // Each wave gathers all logits and runs the top-k itself, so the routing
+    // needs no LDS broadcast and no barrier.  The down row of (this wave's
+    // output row, expert of slot s) is issued in round s, so HBM streams while
+    // the remaining rounds run.  Lane s keeps slot s (expert, route weight).
+    // Lane l holds the logits of experts EL*l .. EL*l + EL-1 (16-byte loads of
+    // two tagged words each).
+    const rsrc_t lr = make_rsrc(w.logits, uint32_t(E) * 8u);
+    u32x4 word[EL / 2];
+    bool ok = true;
+    for (unsigned polls = 0;;) {
+#pragma unroll
+      for (int m = 0; m < EL / 2; ++m) word[m] = buf_load16<kAuxCoherent>(lr, uint32_t(EL * lane + 2 * m) * 8u);
+      bool ready = true;
+#pragma unroll
+      for (int m = 0; m < EL / 2; ++m) {
+        const int e = EL * lane + 2 * m;
+        ready = ready & (e >= E || word[m].y == tag) & (e + 1 >= E || word[m].w == tag);
+      }
+      if (__all(ready)) break;
+      if (++polls >= kSpinLimit) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok && lane == 0) misc[16] = 1;
+    uint32_t key[EL];
+#pragma unroll
+    for (int m = 0; m < EL / 2; ++m) {
+      const int e = EL * lane + 2 * m;
+      key[2 * m] = (ok && e < E) ? ord_key(__uint_as_float(word[m].x)) : 0u;
+      key[2 * m + 1] = (ok && e + 1 < E) ? ord_key(__uint_as_float(word[m].z)) : 0u;
+    }
+    float my_v = 0.f;
+    int my_e = 0;
+    // One top-k round: the wave-wide max of the lanes' largest remaining keys
+    // (0 = absent or taken), then the lowest lane holding it and, in that
+    // lane, its lowest slot -- i.e. the lowest expert index, the reference's
+    // tie rule.  Returns the wave-uniform expert of slot s.  The softmax over
+    // the K selected logits is taken once afterwards, all slots in parallel.
+    auto route_round = [&](int s) -> int {
+      uint32_t lk = key[0];
+#pragma unroll
+      for (int j = 1; j < EL; ++j) lk = max(lk, key[j]);
+      const uint32_t best = wave_max_u32(lk);
+      int jsel = EL - 1;
+#pragma unroll
+      for (int j = EL - 2; j >= 0; --j) jsel = key[j] == best ? j : jsel;
+      const unsigned long long m = __ballot(lk == best);
+      const int L = m != 0ull ? int(__builtin_ctzll(m)) : 0;
+      const int j_l = __builtin_amdgcn_readlane(jsel, L);
+#pragma unroll
+      for (int j = 0; j < EL; ++j) key[j] = (lane == L && j == j_l) ? 0u : key[j];
+      const int bi = EL * L + j_l;
+      const int e = (best != 0u && bi < E) ? bi : 0;
+      if (lane == s) {
+        my_e = e;
+        my_v = ord_value(best);
+      }
+      return e;
+    };
+    const size_t hrow = size_t(min(h0 + wave, H - 1));
+    u32x4 dn[kDN][IC];
+#pragma unroll
+    for (int s = 0; s < kDN; ++s) {
+      int e = 0;
+      if (s < K) e = route_round(s);
+      load_row<T, VEC, IC>(a.ed + (size_t(e) * H + hrow) * I, I, s < K && wave < nrows, lane, dn[s]);
+      pin_loads();
+    }
+    for (int s = kDN; s < K; ++s) route_round(s);
+    // Slot 0 holds the largest logit; exp(v_s - v_0) summed in slot order.
+    const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
+    const float ex = lane < K ? expf(my_v - first) : 0.f;
+    float denom = 0.f;
+    for (int s = 0; s < K; ++s) denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), s));
+    const float my_w = ex / denom;
+    if (wg == 0 && wave == 0 && lane < K) {
+      a.idx[lane] = my_e;
+      a.wts[lane] = my_w;
+    }
+    auto slot_expert = [&](int u) { return __builtin_amdgcn_readlane(my_e, u); };
+    auto slot_weight = [&](int u) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), u)); };
+
+    // Routed gate/up: task t = (slot t / I, row t % I), t = gw + nw_total * m.
+    const int nw_total = nwg * kWaves;
+    const int gw = wave * nwg + wg;
+    const int ntask = K * I;
+    const int step = nw_total * kGU;
+    auto issue_gu = [&](int t0, u32x4 (&g)[kGU][HC], u32x4 (&u)[kGU][HC]) {
+#pragma unroll
+      for (int q = 0; q < kGU; ++q) {
+        const int t = t0 + q * nw_total;
+        const int tc = min(t, ntask - 1);
+        const size_t ro = (size_t(slot_expert(tc / I)) * I + tc % I) * H;
+        load_row<T, VEC, HC>(a.eg + ro, H, t < ntask, lane, g[q]);
+        load_row<T, VEC, HC>(a.eu + ro, H, t < ntask, lane, u[q]);
+      }
+    };
+    auto compute_gu = [&](int t0, const u32x4 (&g)[kGU][HC], const u32x4 (&u)[kGU][HC]) {
+#pragma unroll
+      for (int q = 0; q < kGU; ++q) {
+        const int t = t0 + q * nw_total;
+        if (t < ntask) {
+          const int su = t / I, i = t % I;
+          float gv = dot_row<T, HC>(g[q], xn, H, lane);
+          float uv = dot_row<T, HC>(u[q], xn, H, lane);
+          wave_sum2_u(gv, uv);
+          if (lane == 0) put_tagged(w.act + size_t(su) * I + i, slot_weight(su) * silu(gv) * uv, tag);
+        }
+      }
+    };
+    u32x4 gA[kGU][HC], uA[kGU][HC], gB[kGU][HC], uB[kGU][HC];
+    issue_gu(gw, gA, uA);
+    issue_shared_down();
+    pin_loads();
+    publish_shared();
+    for (int t0 = gw; t0 < ntask; t0 += 2 * step) {
+      if (t0 + step < ntask) issue_gu(t0 + step, gB, uB);
+      pin_loads();
+      compute_gu(t0, gA, uA);
+      if (t0 + step >= ntask) break;
+      if (t0 + 2 * step < ntask) issue_gu(t0 + 2 * step, gA, uA);
+      pin_loads();
+      compute_gu(t0 + step, gB, uB);
+    }
+
+    // ---- phase 3, one batch row ----------------------------------------------
+    // act [K][Ip] and the shared act [Isp] sit after x_norm in LDS (the host
+    // checks they fit), so no barrier is needed before gathering them.
+    float* act1 = xn + Hp;
+    float* sact1 = act1 + size_t(K) * Ip;
+    bool ok3 = true;
+    if constexpr (VEC) {
+      const int hpi = Ip / 2, hps = Isp / 2;  // word pairs per row
+      ok3 = gather_tagged_pairs(
+          make_rsrc(w.sact, uint32_t(Is) * 8u), hps,
+          [&](int f) -> uint32_t { return 2 * f < Is ? uint32_t(2 * f) * 8u : 0xFFFFFFF0u; }, sact1, tag, tid);
+      ok3 = gather_tagged_pairs(
+                make_rsrc(w.act, uint32_t(K) * uint32_t(I) * 8u), K * hpi,
+                [&](int f) -> uint32_t {
+                  const int en = f / hpi, c2 = (f % hpi) * 2;
+                  return c2 < I ? uint32_t(en * I + c2) * 8u : 0xFFFFFFF0u;
+                },
+                act1, tag, tid) &&
+            ok3;
+    } else {
+      for (int t = tid; t < Isp + K * Ip; t += kThreads) {
+        const bool is_sact = t < Isp;
+        const int en = is_sact ? 0 : (t - Isp) / Ip, i = is_sact ? t : (t - Isp) % Ip;
+        const int n = is_sact ? Is : I;
+        float val = 0.f;
+        if (i < n) {
+          const uint64_t* pw = is_sact ? w.sact + i : w.act + size_t(en) * I + i;
+          uint64_t word64 = 0;
+          for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
+            word64 = __hip_atomic_load(const_cast<uint64_t*>(pw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (unsigned(word64 >> 32) == tag) break;
+            __builtin_amdgcn_s_sleep(1);
+          }
+          ok3 = ok3 && unsigned(word64 >> 32) == tag;
+          val = __uint_as_float(unsigned(word64));
+        }
+        if (is_sact)
+          sact1[i] = val;
+        else
+          act1[size_t(en) * Ip + i] = val;
+      }
+    }
+    if (!ok3) misc[16] = 1;
+    __syncthreads();
+    const bool timed_out = misc[16] != 0;
+    if (timed_out && tid == 0) __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Wave w owns output rows h0 + w, h0 + w + kWaves, ...: experts in slot
+    // order (the reference's order), then the gated shared expert and the
+    // residual.
+    // Lane-partial sums of all experts and of the gated shared expert, then a
+    // single wave reduction (the per-expert partials are independent chains).
+    for (int hl = wave; hl < nrows; hl += kWaves) {
+      float part = 0.f;
+      int u0 = 0;
+      if (hl == wave) {
+        // rows of slots >= K were loaded as zeros
+        float pe[kDN];
+#pragma unroll
+        for (int uu = 0; uu < kDN; ++uu) pe[uu] = dot_row<T, IC>(dn[uu], act1 + size_t(min(uu, K - 1)) * Ip, I, lane);
+#pragma unroll
+        for (int st = 1; st < kDN; st *= 2)
+#pragma unroll
+          for (int j = 0; j + st < kDN; j += 2 * st) pe[j] += pe[j + st];
+        part = pe[0];
+        u0 = kDN;
+      }
+      for (int u = u0; u < K; ++u) {
+        u32x4 c[IC];
+        load_row<T, VEC, IC>(a.ed + (size_t(slot_expert(u)) * H + h0 + hl) * I, I, true, lane, c);
+        part += dot_row<T, IC>(c, act1 + size_t(u) * Ip, I, lane);
+      }
+      u32x4 c[IC];
+      if (hl == wave) {
+#pragma unroll
+        for (int q = 0; q < IC; ++q) c[q] = sdn[q];
+      } else {
+        load_row<T, VEC, IC>(a.sd + size_t(h0 + hl) * Is, Is, true, lane, c);
+      }
+      float s = wave_sum_u(fmaf(sgf[0], dot_row<T, IC>(c, sact1, Is, lane), part));
+      const size_t o = size_t(h0 + hl);
+      if (lane == 0) {
+        if (a.add_residual) s += hl == wave ? x_res : to_f(a.x[o]);
+        a.out[o] = from_f<T>(timed_out ? NAN : s);
+      }
+    }
+  } else {
 
   // ---- phase 1: gather the router logits, top-k -----------------------------
   if (wave < B) {
@@ -598,9 +866,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // Double-buffered: the next group is in flight while this one is reduced.
   for (int t0 = gw; t0 < ntask; t0 += 2 * step) {
     if (t0 + step < ntask) issue_gu(t0 + step, gB, uB);
+    pin_loads();
     compute_gu(t0, gA, uA);
     if (t0 + step >= ntask) break;
     if (t0 + 2 * step < ntask) issue_gu(t0 + 2 * step, gA, uA);
+    pin_loads();
     compute_gu(t0 + step, gB, uB);
   }
   // Down rows of (output row h0 + wave, expert u = j), issued only now: they
@@ -611,6 +881,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   for (int j = 0; j < kDN; ++j)
     load_row<T, VEC, IC>(a.ed + (size_t(ulist[min(j, U - 1)]) * H + min(h0 + wave, H - 1)) * I, I,
                          j < U && wave < nrows, lane, dn[j]);
+  pin_loads();
   __syncthreads();  // x_norm (region A) is dead from here on
 
   // ---- phase 3: gather act, down projection --------------------------------
@@ -757,6 +1028,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         }
       }
   }
+  }  // multi-row path
   // WG 0 advances the generation once every WG of this launch has read it.
   if (wg == 0 && wave == 0) {
     const rsrc_t pr = make_rsrc(w.presence, uint32_t(nwg) * 8u);
@@ -807,7 +1079,13 @@ int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
   // Chunk counts per lane: the smallest instantiation that covers the rows.
   const int hc_need = (a.H + EPC * kWave - 1) / (EPC * kWave);
   const int ic_need = (max(a.I, a.Is) + EPC * kWave - 1) / (EPC * kWave);
-  const int which = (vec && hc_need <= 4 && ic_need <= 1) ? (batch == 1 ? 0 : 1) : (vec ? 2 : 3);
+  // The one-row path keeps x_norm, act [K][Ip] and the shared act side by side
+  // in the LDS region that the multi-row path shares between them.
+  const size_t one_row_floats = size_t(round_up(a.H, EPC)) + size_t(a.K) * round_up(a.I, EPC) + round_up(a.Is, EPC);
+  const size_t region_floats = max(size_t(kMaxB) * round_up(a.H, EPC),
+                                   size_t(kActWindowBytes / 4) + size_t(kMaxB) * round_up(a.Is, EPC));
+  const bool one_row_ok = batch == 1 && one_row_floats <= region_floats;
+  const int which = (vec && hc_need <= 4 && ic_need <= 1) ? (one_row_ok ? 0 : 1) : (vec ? 2 : 3);
   const bool el4 = a.E <= 4 * kWave;
   void (*kern)(MoeArgs<T>) = which == 0   ? (el4 ? &moe_decode_kernel<T, true, 4, 1, 1, 4>
                                                  : &moe_decode_kernel<T, true, 4, 1, 1, kMaxEL>)
