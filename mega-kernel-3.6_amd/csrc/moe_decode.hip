@@ -485,90 +485,99 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   if constexpr (MB == 1) {
     issue_shared_gu();
     pin_loads();
-    // ---- phases 1-2, one batch row: every wave routes on its own ------------
-    // Each wave gathers all logits and runs the top-k itself, so the routing
-    // needs no LDS broadcast and no barrier.  The down row of (this wave's
-    // output row, expert of slot s) is issued in round s, so HBM streams while
-    // the remaining rounds run.  Lane s keeps slot s (expert, route weight).
-    // Lane l holds the logits of experts EL*l .. EL*l + EL-1 (16-byte loads of
-    // two tagged words each).
-    const rsrc_t lr = make_rsrc(w.logits, uint32_t(E) * 8u);
-    u32x4 word[EL / 2];
-    bool ok = true;
-    for (unsigned polls = 0;;) {
+    // ---- phases 1-2, one batch row ---------------------------------------------
+    // Wave 0 gathers all logits and routes; the other waves wait at the
+    // barrier below (one polling wave per WG keeps the coherent read traffic
+    // of the exchange 8x lower than every wave polling).  Lane l holds the
+    // logits of experts EL*l .. EL*l + EL-1 (16-byte loads of two tagged
+    // words each), sorted in the lane by (logit descending, index ascending).
+    // A top-k round is then one wave-wide max of the lane heads and a ballot
+    // for the lowest lane holding it -- the lowest expert index among equal
+    // logits, the reference's tie rule -- after which that lane pops its head.
+    // Lane s keeps slot s (expert, logit); the softmax over the K selected
+    // logits is taken once at the end, all slots in parallel.
+    if (wave == 0) {
+      const rsrc_t lr = make_rsrc(w.logits, uint32_t(E) * 8u);
+      u32x4 word[EL / 2];
+      bool ok = true;
+      for (unsigned polls = 0;;) {
 #pragma unroll
-      for (int m = 0; m < EL / 2; ++m) word[m] = buf_load16<kAuxCoherent>(lr, uint32_t(EL * lane + 2 * m) * 8u);
-      bool ready = true;
+        for (int m = 0; m < EL / 2; ++m) word[m] = buf_load16<kAuxCoherent>(lr, uint32_t(EL * lane + 2 * m) * 8u);
+        bool ready = true;
+#pragma unroll
+        for (int m = 0; m < EL / 2; ++m) {
+          const int e = EL * lane + 2 * m;
+          ready = ready & (e >= E || word[m].y == tag) & (e + 1 >= E || word[m].w == tag);
+        }
+        if (__all(ready)) break;
+        if (++polls >= kSpinLimit) {
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!ok && lane == 0) misc[16] = 1;
+      uint32_t key[EL];
+      int kid[EL];
 #pragma unroll
       for (int m = 0; m < EL / 2; ++m) {
         const int e = EL * lane + 2 * m;
-        ready = ready & (e >= E || word[m].y == tag) & (e + 1 >= E || word[m].w == tag);
+        key[2 * m] = (ok && e < E) ? ord_key(__uint_as_float(word[m].x)) : 0u;
+        key[2 * m + 1] = (ok && e + 1 < E) ? ord_key(__uint_as_float(word[m].z)) : 0u;
+        kid[2 * m] = e;
+        kid[2 * m + 1] = e + 1;
       }
-      if (__all(ready)) break;
-      if (++polls >= kSpinLimit) {
-        ok = false;
-        break;
+      // Odd-even transposition sort of the lane's EL keys.
+#pragma unroll
+      for (int r = 0; r < EL; ++r)
+#pragma unroll
+        for (int j = r & 1; j + 1 < EL; j += 2) {
+          const bool sw = key[j + 1] > key[j] || (key[j + 1] == key[j] && kid[j + 1] < kid[j]);
+          const uint32_t k0 = key[j], k1 = key[j + 1];
+          const int i0 = kid[j], i1 = kid[j + 1];
+          key[j] = sw ? k1 : k0;
+          key[j + 1] = sw ? k0 : k1;
+          kid[j] = sw ? i1 : i0;
+          kid[j + 1] = sw ? i0 : i1;
+        }
+      float my_v = 0.f;
+      int my_e = 0;
+      for (int s = 0; s < K; ++s) {
+        const uint32_t best = wave_max_u32(key[0]);
+        const unsigned long long m = __ballot(key[0] == best);
+        const int L = m != 0ull ? int(__builtin_ctzll(m)) : 0;
+        const int e = __builtin_amdgcn_readlane(kid[0], L);
+        const bool pop = lane == L;
+#pragma unroll
+        for (int j = 0; j + 1 < EL; ++j) {
+          key[j] = pop ? key[j + 1] : key[j];
+          kid[j] = pop ? kid[j + 1] : kid[j];
+        }
+        key[EL - 1] = pop ? 0u : key[EL - 1];
+        if (lane == s) {
+          my_e = (best != 0u && e < E) ? e : 0;  // 0 = absent (timed-out wait)
+          my_v = ord_value(best);
+        }
       }
-      __builtin_amdgcn_s_sleep(1);
+      // Slot 0 holds the largest logit; exp(v_s - v_0) summed in slot order.
+      const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
+      const float ex = lane < K ? expf(my_v - first) : 0.f;
+      float denom = 0.f;
+      for (int s = 0; s < K; ++s) denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), s));
+      const float my_w = ex / denom;
+      if (lane < K) {
+        sel_e[lane] = my_e;
+        sel_w[lane] = my_w;
+        if (wg == 0) {
+          a.idx[lane] = my_e;
+          a.wts[lane] = my_w;
+        }
+      }
     }
-    if (!ok && lane == 0) misc[16] = 1;
-    uint32_t key[EL];
-#pragma unroll
-    for (int m = 0; m < EL / 2; ++m) {
-      const int e = EL * lane + 2 * m;
-      key[2 * m] = (ok && e < E) ? ord_key(__uint_as_float(word[m].x)) : 0u;
-      key[2 * m + 1] = (ok && e + 1 < E) ? ord_key(__uint_as_float(word[m].z)) : 0u;
-    }
-    float my_v = 0.f;
-    int my_e = 0;
-    // One top-k round: the wave-wide max of the lanes' largest remaining keys
-    // (0 = absent or taken), then the lowest lane holding it and, in that
-    // lane, its lowest slot -- i.e. the lowest expert index, the reference's
-    // tie rule.  Returns the wave-uniform expert of slot s.  The softmax over
-    // the K selected logits is taken once afterwards, all slots in parallel.
-    auto route_round = [&](int s) -> int {
-      uint32_t lk = key[0];
-#pragma unroll
-      for (int j = 1; j < EL; ++j) lk = max(lk, key[j]);
-      const uint32_t best = wave_max_u32(lk);
-      int jsel = EL - 1;
-#pragma unroll
-      for (int j = EL - 2; j >= 0; --j) jsel = key[j] == best ? j : jsel;
-      const unsigned long long m = __ballot(lk == best);
-      const int L = m != 0ull ? int(__builtin_ctzll(m)) : 0;
-      const int j_l = __builtin_amdgcn_readlane(jsel, L);
-#pragma unroll
-      for (int j = 0; j < EL; ++j) key[j] = (lane == L && j == j_l) ? 0u : key[j];
-      const int bi = EL * L + j_l;
-      const int e = (best != 0u && bi < E) ? bi : 0;
-      if (lane == s) {
-        my_e = e;
-        my_v = ord_value(best);
-      }
-      return e;
-    };
+    __syncthreads();
+    auto slot_expert = [&](int u) { return __builtin_amdgcn_readfirstlane(sel_e[u]); };
+    auto slot_weight = [&](int u) { return sel_w[u]; };
     const size_t hrow = size_t(min(h0 + wave, H - 1));
-    u32x4 dn[kDN][IC];
-#pragma unroll
-    for (int s = 0; s < kDN; ++s) {
-      int e = 0;
-      if (s < K) e = route_round(s);
-      load_row<T, VEC, IC>(a.ed + (size_t(e) * H + hrow) * I, I, s < K && wave < nrows, lane, dn[s]);
-      pin_loads();
-    }
-    for (int s = kDN; s < K; ++s) route_round(s);
-    // Slot 0 holds the largest logit; exp(v_s - v_0) summed in slot order.
-    const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
-    const float ex = lane < K ? expf(my_v - first) : 0.f;
-    float denom = 0.f;
-    for (int s = 0; s < K; ++s) denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), s));
-    const float my_w = ex / denom;
-    if (wg == 0 && wave == 0 && lane < K) {
-      a.idx[lane] = my_e;
-      a.wts[lane] = my_w;
-    }
-    auto slot_expert = [&](int u) { return __builtin_amdgcn_readlane(my_e, u); };
-    auto slot_weight = [&](int u) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), u)); };
 
     // Routed gate/up: task t = (slot t / I, row t % I), t = gw + nw_total * m.
     const int nw_total = nwg * kWaves;
@@ -600,7 +609,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     };
     u32x4 gA[kGU][HC], uA[kGU][HC], gB[kGU][HC], uB[kGU][HC];
     issue_gu(gw, gA, uA);
-    issue_shared_down();
     pin_loads();
     publish_shared();
     for (int t0 = gw; t0 < ntask; t0 += 2 * step) {
@@ -612,6 +620,17 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       pin_loads();
       compute_gu(t0 + step, gB, uB);
     }
+    // Down rows of (this wave's output row, expert of slot s) and the shared
+    // down row: needed only after the act exchange, so they are issued once
+    // this wave's gate/up rows are consumed and stream during the exchange
+    // instead of competing with the gate/up rows that the exchange waits for.
+    u32x4 dn[kDN][IC];
+#pragma unroll
+    for (int s = 0; s < kDN; ++s)
+      load_row<T, VEC, IC>(a.ed + (size_t(slot_expert(min(s, K - 1))) * H + hrow) * I, I, s < K && wave < nrows, lane,
+                           dn[s]);
+    issue_shared_down();
+    pin_loads();
 
     // ---- phase 3, one batch row ----------------------------------------------
     // act [K][Ip] and the shared act [Isp] sit after x_norm in LDS (the host
