@@ -18,12 +18,14 @@
  *   state [batch, v_heads, key_dim, value_dim] float32.
  * All weight/activation pointers of one call share the element type `dtype`.
  *
- * Workspace: entry points that need scratch take (workspace, workspace_bytes);
- * *_workspace_bytes() gives the size.  The caller zero-fills a workspace once,
- * before its first use; every call returns the workspace's counters to zero
- * before its last kernel exits, so the same buffer can be reused by the next
- * call on the same stream without clearing.  Two calls that run concurrently
- * (different streams) must not share a workspace.
+ * Workspace: entry points that need scratch take (workspace, workspace_bytes),
+ * 256-byte aligned; *_workspace_bytes() gives the size.  The caller zero-fills
+ * a workspace once, before its first use, and gives it to one entry point
+ * only: every call leaves the state it keeps there (arrival counters back at
+ * zero, the MoE generation word advanced) ready for the next call of the same
+ * entry point on the same stream, with any shape, so it need not be cleared
+ * again.  Another entry point's scratch data would overwrite that state.  Two
+ * calls that run concurrently (different streams) must not share a workspace.
  */
 #ifndef MKQ_H_
 #define MKQ_H_

@@ -19,6 +19,8 @@
 //      same number of items.  The first items' weight loads are issued before
 //      the act vector is staged in LDS, the quarter sums meet in LDS, and one
 //      barrier finishes the block.
+#include <type_traits>
+
 #include "mkq_host.h"
 
 using namespace mkq;
@@ -325,6 +327,418 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Batched path (3..8 rows per pass): bf16/f16 MFMA, every weight byte read
+// once per pass.
+//
+// Each GEMV  y[n, b] = sum_k W[n, k] v[b, k]  runs as 16x16x32 MFMAs with
+// 16-row tiles of W as the A operand and the vectors as the B operand.  The
+// 16 B columns hold the rows' values split into a 16-bit high part (columns
+// 0..7) and the 16-bit rounding remainder (columns 8..15), so hi + lo carries
+// about 16 mantissa bits of the FP32 x_norm and act.  The B operand is kept
+// in "fragment" order in the workspace: k-step s (32 k values) is 64 lanes x
+// 16 bytes, lane l = column (l % 16) with k = 32 s + 8 (l / 16) .. + 7, so a
+// wave fetches it with one coalesced 1 KB load per step (L2 hits).
+//
+// Weights are not loaded in the A-operand layout (16 rows x 64 bytes per
+// instruction, twice the cache-line requests per byte): each load instruction
+// reads two rows' 512-byte segments (4 full 128-byte lines each), the wave
+// writes them to its own LDS area and reads the A operands back transposed.
+// A wave owns two 16-row tiles, so each B fragment load serves two MFMAs.
+//
+// Work units are (32-row pair of tiles, k-split) workgroups -- a few thousand,
+// so the dispatcher balances them over the CUs; the 4 waves of a workgroup
+// split its k range further and meet in LDS.  The k-split partials of a pair
+// meet through a per-pair arrival counter: the workgroup that arrives last
+// adds them (agent-coherent stores and loads), applies the epilogue (SwiGLU
+// into the down projection's B fragments, or residual + rounding into out)
+// and returns the counter to zero for the next call.
+//
+//   K0 ffn_pack_x_kernel       RMSNorm of the rows -> x_norm fragments
+//   K1 ffn_gateup_mfma_kernel  gate and up -> act fragments   (4 k-splits)
+//   K2 ffn_down_mfma_kernel    down -> out (+ residual)      (8 k-splits)
+// ---------------------------------------------------------------------------
+constexpr int kMfmaRows = 8;         // batch rows per pass (columns 0..7 hi, 8..15 lo)
+constexpr int kMfmaMinBatch = 3;     // smaller batches take the row-GEMV kernels above
+constexpr int kPairRows = 32;        // rows per workgroup (two 16-row tiles per wave)
+constexpr int kSplit1 = 4;           // k-splits of gate/up (workgroups per pair)
+constexpr int kSplit2 = 8;           // k-splits of down
+constexpr int kStepBatch = 8;        // k-steps per load batch: 256 k = 512 bytes per row
+constexpr int kLdsRow = 512 + 16;    // LDS stride of a staged row segment (bytes; conflict-free reads)
+constexpr int kWaveLds = kPairRows * kLdsRow;  // staged bytes per wave
+constexpr int kMaxPairs1 = 4096;     // intermediate <= 131072
+constexpr int kMaxPairs2 = 2048;     // hidden <= 65536
+constexpr int kPackThreads = 1024;   // K0: one k-step per wave
+constexpr int kPackUnroll = 8;       // K0: x chunks in flight per thread
+constexpr uint32_t kFarOff = 0x80000000u;
+
+template <typename T>
+struct MfmaOp;
+template <>
+struct MfmaOp<bf16_t> {
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+  }
+  // 16-bit high part and remainder of v.
+  static __device__ __forceinline__ void split(float v, uint16_t& hi, uint16_t& lo) {
+    hi = f2bf_bits(v);
+    lo = f2bf_bits(v - __uint_as_float(uint32_t(hi) << 16));
+  }
+};
+template <>
+struct MfmaOp<f16_t> {
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                 0);
+  }
+  static __device__ __forceinline__ void split(float v, uint16_t& hi, uint16_t& lo) {
+    const _Float16 h = _Float16(v);
+    const _Float16 l = _Float16(v - float(h));
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, l);
+  }
+};
+
+// Workspace of the batched path (bytes from the workspace start).  The
+// counters sit at fixed offsets for every shape, so a workspace reused with
+// another shape still finds them at zero.
+struct MfmaWs {
+  unsigned* cnt1;  // [kMaxPairs1]
+  unsigned* cnt2;  // [kMaxPairs2]
+  uint16_t* xf;    // [s1][64][8]  x_norm fragments
+  uint16_t* af;    // [s2][64][8]  act fragments
+  float* p1;       // [pairs1][kSplit1][2 (gate, up)][32 rows][8 cols]
+  float* p2;       // [pairs2][kSplit2][32 rows][8 cols]
+  size_t bytes;
+};
+
+__host__ __device__ inline size_t align_256(size_t v) { return (v + 255) & ~size_t(255); }
+
+inline MfmaWs mfma_ws(void* base, int h, int inter) {
+  const size_t s1 = (size_t(h) + 31) / 32, s2 = (size_t(inter) + 31) / 32;
+  const size_t n1 = (size_t(inter) + kPairRows - 1) / kPairRows, n2 = (size_t(h) + kPairRows - 1) / kPairRows;
+  unsigned char* p = static_cast<unsigned char*>(base);
+  MfmaWs w;
+  size_t off = 0;
+  w.cnt1 = reinterpret_cast<unsigned*>(p + off);
+  off = align_256(off + 4 * size_t(kMaxPairs1));
+  w.cnt2 = reinterpret_cast<unsigned*>(p + off);
+  off = align_256(off + 4 * size_t(kMaxPairs2));
+  w.xf = reinterpret_cast<uint16_t*>(p + off);
+  off = align_256(off + s1 * 1024);
+  w.af = reinterpret_cast<uint16_t*>(p + off);
+  off = align_256(off + s2 * 1024);
+  w.p1 = reinterpret_cast<float*>(p + off);
+  off = align_256(off + n1 * kSplit1 * 2 * kPairRows * kMfmaRows * 4);
+  w.p2 = reinterpret_cast<float*>(p + off);
+  off = align_256(off + n2 * kSplit2 * kPairRows * kMfmaRows * 4);
+  w.bytes = off;
+  return w;
+}
+
+// K0: grid = ceil(s1 / 16), block 1024; wave w writes the fragment of k-step
+// 16 * blockIdx.x + w.  Every workgroup computes the rows' inverse RMS itself
+// (x is a few KB, read from L2 with all loads of a thread in flight at once).
+template <typename T>
+__global__ __launch_bounds__(kPackThreads) void ffn_pack_x_kernel(const T* __restrict__ x, const T* __restrict__ nw,
+                                                                  uint16_t* __restrict__ xf, int nb, int h, int s1,
+                                                                  float eps) {
+  constexpr int kPackWaves = kPackThreads / kWave;
+  __shared__ float red[kPackWaves][kMfmaRows];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
+  const int hq = h / 8;  // 16-byte chunks per row
+  const rsrc_t xr = make_rsrc(x, uint32_t(nb) * uint32_t(h) * 2u);
+  float ss[kMfmaRows];
+#pragma unroll
+  for (int b = 0; b < kMfmaRows; ++b) ss[b] = 0.f;
+  for (int q0 = tid; q0 < nb * hq; q0 += kPackUnroll * kPackThreads) {
+    u32x4 v[kPackUnroll];
+#pragma unroll
+    for (int r = 0; r < kPackUnroll; ++r) {
+      const int q = q0 + r * kPackThreads;
+      v[r] = buf_load16(xr, q < nb * hq ? uint32_t(q) * 16u : kFarOff);
+    }
+#pragma unroll
+    for (int r = 0; r < kPackUnroll; ++r) {
+      const int b = min((q0 + r * kPackThreads) / hq, kMfmaRows - 1);  // chunks past the rows read zero
+      float f[8];
+      unpack(v[r], f, T{});
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s = fmaf(f[e], f[e], s);
+#pragma unroll
+      for (int bb = 0; bb < kMfmaRows; ++bb) ss[bb] += bb == b ? s : 0.f;
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < kMfmaRows; ++b) {
+    const float t = wave_sum_u(ss[b]);
+    if (lane == 0) red[wave][b] = t;
+  }
+  __syncthreads();
+  const int s = blockIdx.x * kPackWaves + wave;
+  if (s >= s1) return;
+  const int c = lane & 15, kg = lane >> 4;
+  const int b = c & 7;
+  const int k0 = 32 * s + 8 * kg;
+  uint16_t o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (b < nb && k0 < h) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kPackWaves; ++w) t += red[w][b];
+    const float inv = 1.0f / sqrtf(t / float(h) + eps);
+    float xv[8], wv[8];
+    unpack(*reinterpret_cast<const u32x4*>(x + size_t(b) * h + k0), xv, T{});
+    unpack(*reinterpret_cast<const u32x4*>(nw + k0), wv, T{});
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint16_t hi, lo;
+      MfmaOp<T>::split(xv[e] * inv * wv[e], hi, lo);
+      o[e] = c < 8 ? hi : lo;
+    }
+  }
+  u32x4 v;
+  v.x = uint32_t(o[0]) | (uint32_t(o[1]) << 16);
+  v.y = uint32_t(o[2]) | (uint32_t(o[3]) << 16);
+  v.z = uint32_t(o[4]) | (uint32_t(o[5]) << 16);
+  v.w = uint32_t(o[6]) | (uint32_t(o[7]) << 16);
+  *reinterpret_cast<u32x4*>(xf + (size_t(s) * kWave + lane) * 8) = v;
+}
+
+// Accumulates the products of 32 rows of W (two 16-row tiles; the descriptor
+// `wr` starts at the first row and covers only rows of the matrix, so rows
+// past it read zero) with the B fragments of k-steps [sb, se).  Load
+// instruction i of a batch reads rows 2i (lanes 0..31) and 2i + 1 (lanes
+// 32..63), 512 contiguous bytes each; k past kdim or past se reads zero.
+template <typename T>
+__device__ __forceinline__ void pair_mfma(rsrc_t wr, rsrc_t fr, int kdim, int sb, int se, int lane,
+                                          unsigned char* __restrict__ lds, f32x4 (&acc)[2]) {
+  constexpr int NI = kPairRows / 2;  // load instructions per batch
+  const int half = lane >> 5, cb = (lane & 31) * 16;  // row parity, byte in the 512-byte segment
+  const uint32_t rstride = uint32_t(kdim) * 2u;
+  auto woff = [&](int s0, int i) -> uint32_t {
+    const int s = s0 + cb / 64;                // k-step of the lane's 16 bytes
+    const int k = 32 * s0 + cb / 2;            // first k of the lane's 16 bytes
+    return (s < se && k < kdim) ? uint32_t(2 * i + half) * rstride + uint32_t(k) * 2u : kFarOff;
+  };
+  auto foff = [&](int s) -> uint32_t { return s < se ? (uint32_t(s) * kWave + lane) * 16u : kFarOff; };
+  u32x4 wa[NI], fa[kStepBatch], wb[NI], fb[kStepBatch];
+  auto issue = [&](int s0, u32x4 (&w)[NI], u32x4 (&f)[kStepBatch]) {
+#pragma unroll
+    for (int j = 0; j < kStepBatch; ++j) f[j] = buf_load16(fr, foff(s0 + j));
+#pragma unroll
+    for (int i = 0; i < NI; ++i) w[i] = buf_load16<kAuxStream>(wr, woff(s0, i));
+  };
+  // Stage the batch (row 2i + half at byte cb), then read the A operands:
+  // tile t, lane l = row 16 t + (l % 16), k-step j, bytes 64 j + 16 (l / 16).
+  unsigned char* wst = lds + (half * kLdsRow + cb);
+  const unsigned char* rd = lds + ((lane & 15) * kLdsRow + 16 * (lane >> 4));
+  auto consume = [&](const u32x4 (&w)[NI], const u32x4 (&f)[kStepBatch]) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4*>(wst + 2 * i * kLdsRow) = w[i];
+#pragma unroll
+    for (int j = 0; j < kStepBatch; ++j)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(rd + 16 * t * kLdsRow + 64 * j);
+        acc[t] = MfmaOp<T>::mma(a, f[j], acc[t]);
+      }
+  };
+  acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The next batch is always issued (steps past se are out-of-range loads:
+  // zeros, no memory traffic), so the loop body has no branch and the waits
+  // before a batch's use cover only that batch.
+  issue(sb, wa, fa);
+  pin_loads();
+  for (int s0 = sb; s0 < se; s0 += 2 * kStepBatch) {
+    issue(s0 + kStepBatch, wb, fb);
+    pin_loads();
+    consume(wa, fa);
+    issue(s0 + 2 * kStepBatch, wa, fa);
+    pin_loads();
+    consume(wb, fb);
+  }
+}
+
+// Adds the lo columns (8..15) onto the hi columns (0..7) of an MFMA result:
+// lane l (column l % 16, rows 4 (l / 16) + i) gets the value of lane l + 8.
+__device__ __forceinline__ f32x4 fold_hi_lo(f32x4 a) {
+  f32x4 r;
+  r[0] = a[0] + dpp<0x128>(a[0]);
+  r[1] = a[1] + dpp<0x128>(a[1]);
+  r[2] = a[2] + dpp<0x128>(a[2]);
+  r[3] = a[3] + dpp<0x128>(a[3]);
+  return r;
+}
+
+// Partials cross workgroups (and XCDs) through agent-coherent accesses: the
+// stores write through to memory and the loads bypass the XCD-private L2
+// copies, so no cache writeback or invalidation (an agent-scope fence) is
+// needed.
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Per-pair arrival: each thread waits until its partial stores are complete
+// (acknowledged by memory), the barrier gathers the workgroup, then one
+// thread counts the arrival; the workgroup learns whether it came last.  A
+// workgroup that reads the final count reads the partials only after it, so
+// it sees every split's complete stores.
+__device__ __forceinline__ bool arrive_last(unsigned* cnt, unsigned splits, int* flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1u ? 1 : 0;
+  __syncthreads();
+  return *flag != 0;
+}
+
+// Writes the 32x8 hi/lo-folded results of the workgroup's 4 waves (two tiles
+// each) to LDS: red[wave][row][col].
+__device__ __forceinline__ void stash_pair(const f32x4 (&acc)[2], float (*red)[kPairRows][kMfmaRows], int wave,
+                                           int lane) {
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const f32x4 v = fold_hi_lo(acc[t]);
+    if (c < kMfmaRows) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][16 * t + 4 * g + i][c] = v[i];
+    }
+  }
+}
+
+// K1: grid = pairs1 * kSplit1, block 256.  blockIdx = kSplit1 * pair + split;
+// wave w computes matrix (w >> 1: gate, up) over part 2 * split + (w & 1) of
+// 2 * kSplit1 equal parts of k.
+template <typename T>
+__global__ __launch_bounds__(kThreads, 2) void ffn_gateup_mfma_kernel(const T* __restrict__ wg,
+                                                                      const T* __restrict__ wu,
+                                                                      const uint16_t* __restrict__ xf,
+                                                                      uint16_t* __restrict__ af,
+                                                                      float* __restrict__ p1,
+                                                                      unsigned* __restrict__ cnt1, int nb, int h,
+                                                                      int inter) {
+  __shared__ __attribute__((aligned(16))) unsigned char stage[kWaves * kWaveLds];
+  __shared__ float red[kWaves][kPairRows][kMfmaRows];
+  __shared__ int flag;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
+  const int pair = blockIdx.x / kSplit1, q = blockIdx.x % kSplit1;
+  const int s1 = (h + 31) / 32;
+  const int part = 2 * q + (wave & 1);
+  const int sb = part * s1 / (2 * kSplit1), se = (part + 1) * s1 / (2 * kSplit1);
+  const int r0 = kPairRows * pair;
+  const int rows = min(kPairRows, inter - r0);
+  const T* w = (wave >> 1) ? wu : wg;
+  const rsrc_t wr = make_rsrc(w + size_t(r0) * h, uint32_t(rows) * uint32_t(h) * 2u);
+  const rsrc_t fr = make_rsrc(xf, uint32_t(s1) * 1024u);
+  f32x4 acc[2];
+  pair_mfma<T>(wr, fr, h, sb, se, lane, stage + wave * kWaveLds, acc);
+  stash_pair(acc, red, wave, lane);
+  __syncthreads();
+  constexpr int kPart = 2 * kPairRows * kMfmaRows;  // floats per (pair, split)
+  float* pt = p1 + size_t(pair) * kSplit1 * kPart;
+  {
+    const int r = tid / kMfmaRows, b = tid % kMfmaRows;  // tid < 256 = 32 rows x 8 columns
+    store_partial(pt + q * kPart + tid, red[0][r][b] + red[1][r][b]);
+    store_partial(pt + q * kPart + kPairRows * kMfmaRows + tid, red[2][r][b] + red[3][r][b]);
+  }
+  if (!arrive_last(cnt1 + pair, kSplit1, &flag)) return;
+  // Last split of this pair: act = silu(gate) * up for its 32 rows, written
+  // as the down projection's B fragments (k = intermediate index); rows past
+  // `inter` (up to the next multiple of 32) and columns past nb are zero.
+  {
+    const int r = tid / kMfmaRows, b = tid % kMfmaRows;
+    const int i = r0 + r;
+    float gs = 0.f, us = 0.f;
+#pragma unroll
+    for (int qq = 0; qq < kSplit1; ++qq) {
+      gs += load_partial(pt + qq * kPart + tid);
+      us += load_partial(pt + qq * kPart + kPairRows * kMfmaRows + tid);
+    }
+    uint16_t hi = 0, lo = 0;
+    if (b < nb && i < inter) MfmaOp<T>::split(silu(gs) * us, hi, lo);
+    const int s = i / 32, kg = (i % 32) / 8, j = i % 8;
+    af[(size_t(s) * kWave + b + 16 * kg) * 8 + j] = hi;
+    af[(size_t(s) * kWave + b + 8 + 16 * kg) * 8 + j] = lo;
+  }
+  if (tid == 0) __hip_atomic_store(cnt1 + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// K2: grid = pairs2 * kSplit2, block 256.  blockIdx = kSplit2 * pair + split;
+// wave w covers part 4 * split + w of 4 * kSplit2 equal parts of k (the
+// intermediate axis).
+template <typename T>
+__global__ __launch_bounds__(kThreads, 2) void ffn_down_mfma_kernel(const T* __restrict__ wd,
+                                                                    const uint16_t* __restrict__ af,
+                                                                    const T* __restrict__ x, T* __restrict__ out,
+                                                                    float* __restrict__ p2,
+                                                                    unsigned* __restrict__ cnt2, int nb, int h,
+                                                                    int inter, int add_residual) {
+  __shared__ __attribute__((aligned(16))) unsigned char stage[kWaves * kWaveLds];
+  __shared__ float red[kWaves][kPairRows][kMfmaRows];
+  __shared__ int flag;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
+  const int pair = blockIdx.x / kSplit2, q = blockIdx.x % kSplit2;
+  const int s2 = (inter + 31) / 32;
+  const int part = kWaves * q + wave;
+  const int sb = part * s2 / (kWaves * kSplit2), se = (part + 1) * s2 / (kWaves * kSplit2);
+  const int r0 = kPairRows * pair;
+  const int rows = min(kPairRows, h - r0);
+  const rsrc_t wr = make_rsrc(wd + size_t(r0) * inter, uint32_t(rows) * uint32_t(inter) * 2u);
+  const rsrc_t fr = make_rsrc(af, uint32_t(s2) * 1024u);
+  f32x4 acc[2];
+  pair_mfma<T>(wr, fr, inter, sb, se, lane, stage + wave * kWaveLds, acc);
+  stash_pair(acc, red, wave, lane);
+  __syncthreads();
+  constexpr int kPart = kPairRows * kMfmaRows;
+  float* pt = p2 + size_t(pair) * kSplit2 * kPart;
+  {
+    const int r = tid / kMfmaRows, b = tid % kMfmaRows;
+    store_partial(pt + q * kPart + tid, red[0][r][b] + red[1][r][b] + red[2][r][b] + red[3][r][b]);
+  }
+  if (!arrive_last(cnt2 + pair, kSplit2, &flag)) return;
+  {
+    const int r = tid / kMfmaRows, b = tid % kMfmaRows;
+    const int n = r0 + r;
+    if (n < h && b < nb) {
+      float s = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < kSplit2; ++qq) s += load_partial(pt + qq * kPart + tid);
+      const size_t o = size_t(b) * h + n;
+      if (add_residual) s += to_f(x[o]);
+      out[o] = from_f<T>(s);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(cnt2 + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+int launch_mfma(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, T* out, int batch, int h, int inter,
+                float eps, int add_residual, const MfmaWs& ws, hipStream_t stream) {
+  const int s1 = (h + 31) / 32;
+  const int n1 = (inter + kPairRows - 1) / kPairRows, n2 = (h + kPairRows - 1) / kPairRows;
+  constexpr int kPackWaves = kPackThreads / kWave;
+  for (int b0 = 0; b0 < batch; b0 += kMfmaRows) {
+    const int nb = batch - b0 < kMfmaRows ? batch - b0 : kMfmaRows;
+    const T* xb = x + size_t(b0) * h;
+    ffn_pack_x_kernel<T><<<(s1 + kPackWaves - 1) / kPackWaves, kPackThreads, 0, stream>>>(xb, nw, ws.xf, nb, h, s1,
+                                                                                          eps);
+    MKQ_LAUNCH_CHECK("ffn_pack_x_kernel");
+    ffn_gateup_mfma_kernel<T><<<kSplit1 * n1, kThreads, 0, stream>>>(wg, wu, ws.xf, ws.af, ws.p1, ws.cnt1, nb, h,
+                                                                     inter);
+    MKQ_LAUNCH_CHECK("ffn_gateup_mfma_kernel");
+    ffn_down_mfma_kernel<T><<<kSplit2 * n2, kThreads, 0, stream>>>(wd, ws.af, xb, out + size_t(b0) * h, ws.p2,
+                                                                   ws.cnt2, nb, h, inter, add_residual);
+    MKQ_LAUNCH_CHECK("ffn_down_mfma_kernel");
+  }
+  return MKQ_OK;
+}
+
 template <typename K>
 int set_lds_limit(K kernel) {
   MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -398,7 +812,7 @@ int dispatch_cpl(const T* x, const T* nw, const T* wg, const T* wu, const T* wd,
 
 template <typename T>
 int dense_ffn_typed(const void* xv, const void* nwv, const void* gv, const void* uv, const void* dv, void* outv,
-                    int batch, int h, int inter, float eps, int add_residual, float* act, hipStream_t stream) {
+                    int batch, int h, int inter, float eps, int add_residual, void* act_base, hipStream_t stream) {
   constexpr int EPC = Epc<T>::value;
   const T* x = static_cast<const T*>(xv);
   const T* nw = static_cast<const T*>(nwv);
@@ -407,6 +821,13 @@ int dense_ffn_typed(const void* xv, const void* nwv, const void* gv, const void*
   const T* wd = static_cast<const T*>(dv);
   T* out = static_cast<T*>(outv);
   const bool vec = (h % EPC == 0) && (inter % EPC == 0) && aligned16(wg) && aligned16(wu) && aligned16(wd);
+  const MfmaWs mws = mfma_ws(act_base, h, inter);
+  float* act = reinterpret_cast<float*>(static_cast<unsigned char*>(act_base) + mws.bytes);
+  if constexpr (!std::is_same<T, float>::value) {
+    if (batch >= kMfmaMinBatch && vec && aligned16(x) && aligned16(nw) && (inter + kPairRows - 1) / kPairRows <= kMaxPairs1 &&
+        (h + kPairRows - 1) / kPairRows <= kMaxPairs2)
+      return launch_mfma<T>(x, nw, wg, wu, wd, out, batch, h, inter, eps, add_residual, mws, stream);
+  }
   for (int b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
     const int nb = batch - b0 >= 2 ? 2 : 1;
     const T* xb = x + size_t(b0) * h;
@@ -427,9 +848,9 @@ int dense_ffn_typed(const void* xv, const void* nwv, const void* gv, const void*
 }  // namespace
 
 extern "C" size_t mkq_dense_ffn_decode_workspace_bytes(int batch, int hidden, int intermediate) {
-  (void)hidden;
-  if (batch <= 0 || intermediate <= 0) return 0;
-  return sizeof(float) * size_t(batch) * size_t(intermediate);
+  if (batch <= 0 || hidden <= 0 || intermediate <= 0) return 0;
+  // batched-path region (counters at fixed offsets first), then act [batch, intermediate]
+  return mfma_ws(nullptr, hidden, intermediate).bytes + sizeof(float) * size_t(batch) * size_t(intermediate);
 }
 
 extern "C" int mkq_dense_ffn_decode(int dtype, const void* x, const void* norm_weight, const void* gate_weight,
@@ -442,8 +863,9 @@ extern "C" int mkq_dense_ffn_decode(int dtype, const void* x, const void* norm_w
               "dense_ffn_decode: null tensor pointer");
   MKQ_REQUIRE(workspace && workspace_bytes >= mkq_dense_ffn_decode_workspace_bytes(batch, hidden, intermediate),
               "dense_ffn_decode: workspace too small");
+  MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "dense_ffn_decode: workspace must be 256-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* act = static_cast<float*>(workspace);
+  void* act = workspace;
   switch (dtype) {
     case MKQ_DTYPE_BF16:
       return dense_ffn_typed<bf16_t>(x, norm_weight, gate_weight, up_weight, down_weight, out, batch, hidden,

@@ -12,6 +12,7 @@
 #include <torch/extension.h>
 
 #include <map>
+#include <tuple>
 #include <utility>
 
 #include "../../include/mkq.h"
@@ -44,12 +45,15 @@ void check_status(int rc, const char* op) {
 
 hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); }
 
-// One zero-filled workspace per (device, stream).  Kernels return every
-// counter they use to zero before exiting, so the buffer is cleared only when
-// it is first allocated (or grown).
-torch::Tensor workspace_for(const torch::Tensor& like, size_t bytes) {
-  static std::map<std::pair<int, hipStream_t>, torch::Tensor> cache;
-  const auto key = std::make_pair(static_cast<int>(like.get_device()), current_stream());
+// One zero-filled workspace per (entry point, device, stream).  Kernels leave
+// the state they keep there (counters, the MoE generation word) ready for the
+// next call of the same entry point, so the buffer is cleared only when it is
+// first allocated (or grown); entry points do not share one, since another
+// entry point's scratch data would overwrite that state.
+enum class Ws { kMoe, kDense, kAttention };
+torch::Tensor workspace_for(Ws op, const torch::Tensor& like, size_t bytes) {
+  static std::map<std::tuple<int, int, hipStream_t>, torch::Tensor> cache;
+  const auto key = std::make_tuple(static_cast<int>(op), static_cast<int>(like.get_device()), current_stream());
   auto it = cache.find(key);
   if (it != cache.end() && static_cast<size_t>(it->second.numel()) >= bytes) return it->second;
   size_t grow = bytes < 4096 ? 4096 : bytes;
@@ -132,7 +136,7 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> moe_impl(
   auto weights = torch::empty({batch, top_k}, x.options().dtype(torch::kFloat32));
   const size_t ws_bytes =
       mkq_moe_decode_workspace_bytes(batch, hidden, experts, intermediate, shared_intermediate, static_cast<int>(top_k));
-  auto ws = workspace_for(x, ws_bytes);
+  auto ws = workspace_for(Ws::kMoe, x, ws_bytes);
   const int rc = mkq_moe_decode(to_mkq_dtype(x), x.data_ptr(), norm_weight.data_ptr(), router_weight.data_ptr(),
                                 expert_gate.data_ptr(), expert_up.data_ptr(), expert_down.data_ptr(),
                                 shared_gate.data_ptr(), shared_up.data_ptr(), shared_down.data_ptr(), sg_ptr,
@@ -184,7 +188,7 @@ torch::Tensor dense_ffn_decode(torch::Tensor x, torch::Tensor norm_weight, torch
   TORCH_CHECK(down_weight.size(0) == hidden && down_weight.size(1) == intermediate, "down_weight shape mismatch");
   c10::DeviceGuard guard(x.device());
   auto out = torch::empty_like(x);
-  auto ws = workspace_for(x, mkq_dense_ffn_decode_workspace_bytes(batch, hidden, intermediate));
+  auto ws = workspace_for(Ws::kDense, x, mkq_dense_ffn_decode_workspace_bytes(batch, hidden, intermediate));
   const int rc = mkq_dense_ffn_decode(to_mkq_dtype(x), x.data_ptr(), norm_weight.data_ptr(), gate_weight.data_ptr(),
                                       up_weight.data_ptr(), down_weight.data_ptr(), out.data_ptr(), batch, hidden,
                                       intermediate, static_cast<float>(eps), add_residual ? 1 : 0, ws.data_ptr(),
@@ -215,7 +219,7 @@ torch::Tensor full_attention_decode(torch::Tensor q, torch::Tensor k_cache, torc
   TORCH_CHECK(seq_len > 0, "seq_len must be positive");
   c10::DeviceGuard guard(q.device());
   auto out = torch::empty_like(q);
-  auto ws = workspace_for(q, mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq_len));
+  auto ws = workspace_for(Ws::kAttention, q, mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq_len));
   const int rc = mkq_full_attention_decode(to_mkq_dtype(q), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                            out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq_len,
                                            static_cast<float>(scale), ws.data_ptr(), static_cast<size_t>(ws.numel()),

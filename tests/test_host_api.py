@@ -63,7 +63,10 @@ def test_c_abi_rejects_bad_arguments_without_gpu():
 
 def test_workspace_sizes():
     lib = _lib.load_library()
-    assert lib.mkq_dense_ffn_decode_workspace_bytes(2, 5120, 17408) == 2 * 17408 * 4
+    # act [batch, intermediate] FP32 plus the batched path's fragments, partials and counters
+    assert lib.mkq_dense_ffn_decode_workspace_bytes(2, 5120, 17408) >= 2 * 17408 * 4 + 17408 // 32 * 1024
+    assert (lib.mkq_dense_ffn_decode_workspace_bytes(8, 5120, 17408)
+            - lib.mkq_dense_ffn_decode_workspace_bytes(2, 5120, 17408)) == 6 * 17408 * 4
     assert lib.mkq_moe_decode_workspace_bytes(1, 2048, 256, 512, 512, 8) > 8 * 8 * 512 * 4
     assert lib.mkq_full_attention_decode_workspace_bytes(1, 24, 4, 256, 32768) >= 24 * 32768 * 4
 
