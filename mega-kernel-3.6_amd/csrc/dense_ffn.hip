@@ -449,6 +449,15 @@ __global__ __launch_bounds__(kPackThreads) void ffn_pack_x_kernel(const T* __res
   const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
   const int hq = h / 8;  // 16-byte chunks per row
   const rsrc_t xr = make_rsrc(x, uint32_t(nb) * uint32_t(h) * 2u);
+  // This lane's fragment inputs are fetched first, so their latency overlaps
+  // the sum-of-squares loads instead of following them.
+  const int s = blockIdx.x * (kPackThreads / kWave) + wave;
+  const int c = lane & 15, kg = lane >> 4;
+  const int b = c & 7;
+  const int k0 = 32 * s + 8 * kg;
+  const bool live = s < s1 && b < nb && k0 < h;
+  const u32x4 xq = buf_load16(xr, live ? (uint32_t(b) * uint32_t(h) + uint32_t(k0)) * 2u : kFarOff);
+  const u32x4 nq = buf_load16(make_rsrc(nw, uint32_t(h) * 2u), live ? uint32_t(k0) * 2u : kFarOff);
   float ss[kMfmaRows];
 #pragma unroll
   for (int b = 0; b < kMfmaRows; ++b) ss[b] = 0.f;
@@ -461,14 +470,14 @@ __global__ __launch_bounds__(kPackThreads) void ffn_pack_x_kernel(const T* __res
     }
 #pragma unroll
     for (int r = 0; r < kPackUnroll; ++r) {
-      const int b = min((q0 + r * kPackThreads) / hq, kMfmaRows - 1);  // chunks past the rows read zero
+      const int rb = min((q0 + r * kPackThreads) / hq, kMfmaRows - 1);  // chunks past the rows read zero
       float f[8];
       unpack(v[r], f, T{});
-      float s = 0.f;
+      float sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s = fmaf(f[e], f[e], s);
+      for (int e = 0; e < 8; ++e) sq = fmaf(f[e], f[e], sq);
 #pragma unroll
-      for (int bb = 0; bb < kMfmaRows; ++bb) ss[bb] += bb == b ? s : 0.f;
+      for (int bb = 0; bb < kMfmaRows; ++bb) ss[bb] += bb == rb ? sq : 0.f;
     }
   }
 #pragma unroll
@@ -477,20 +486,16 @@ __global__ __launch_bounds__(kPackThreads) void ffn_pack_x_kernel(const T* __res
     if (lane == 0) red[wave][b] = t;
   }
   __syncthreads();
-  const int s = blockIdx.x * kPackWaves + wave;
   if (s >= s1) return;
-  const int c = lane & 15, kg = lane >> 4;
-  const int b = c & 7;
-  const int k0 = 32 * s + 8 * kg;
   uint16_t o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (b < nb && k0 < h) {
+  if (live) {
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < kPackWaves; ++w) t += red[w][b];
     const float inv = 1.0f / sqrtf(t / float(h) + eps);
     float xv[8], wv[8];
-    unpack(*reinterpret_cast<const u32x4*>(x + size_t(b) * h + k0), xv, T{});
-    unpack(*reinterpret_cast<const u32x4*>(nw + k0), wv, T{});
+    unpack(xq, xv, T{});
+    unpack(nq, wv, T{});
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       uint16_t hi, lo;

@@ -48,10 +48,11 @@ constexpr int kMaxB = 8;       // batch rows per launch (larger batches are spli
 constexpr int kMaxWg = 1024;   // workgroups
 constexpr int kMaxHC = 8;      // max 16-byte chunks per lane for a hidden-long row (H <= 512*EPC)
 constexpr int kMaxIC = 2;      // max 16-byte chunks per lane for an intermediate-long row (I <= 128*EPC)
-constexpr int kGU = 2;         // routed gate/up row pairs in flight per wave
-constexpr int kDN = 8;         // down rows in flight per wave
+constexpr int kGU = 2;         // routed gate/up row pairs per wave and load group (one-row path)
+constexpr int kGUM = 1;        // the same for the multi-row path, whose per-row state needs the registers
+constexpr int kDN = 8;         // down rows issued per wave before the act hand-off
+constexpr int kDS = 6;         // down rows per streamed group in the multi-row down phase
 constexpr int kMaxEL = 16;     // router logits per lane (E <= 1024)
-constexpr int kActWindowBytes = 64 * 1024;
 constexpr unsigned kSpinLimit = 1u << 21;
 
 // Workspace layout (bytes).  The generation and error words live in their own
@@ -85,6 +86,7 @@ struct MoeArgs {
   int add_residual;
   int nwg;
   int rows_per_wg;  // output rows per WG in phase 3
+  int win_floats;   // act window of the multi-row down phase (floats, a multiple of round_up(I, EPC))
 };
 
 struct WsPtrs {
@@ -125,10 +127,6 @@ __device__ __forceinline__ void put_tagged(uint64_t* p, float v, unsigned tag) {
   __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ u32x2 ld8_coherent(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kAuxCoherent));
-}
 
 // Loads up to MAXC 16-byte chunks per lane of a row of length n (chunk j of
 // the lane is chunk lane + 64*j of the row); chunks past the row, and every
@@ -235,6 +233,85 @@ __device__ bool gather_tagged_pairs(rsrc_t r, int pairs, SrcFn src, float* dst, 
   return ok;
 }
 
+// Routes one batch row (one wave): waits until the E tagged logits behind `lr`
+// carry `tag`, then takes the top K by (logit descending, index ascending) --
+// the reference's order and tie rule -- and the softmax over those K logits.
+// Lane s < K returns slot s (expert, route weight).  Lane l holds the logits of
+// experts EL*l .. EL*l + EL-1 (16-byte loads of two tagged words each), sorted
+// in the lane; a round is then one wave-wide max of the lane heads and a
+// ballot for the lowest lane holding it, after which that lane pops its head.
+// Returns false (experts 0) if the wait timed out.
+template <int EL>
+__device__ bool route_row(rsrc_t lr, int E, int K, unsigned tag, int lane, int& my_e, float& my_w) {
+  u32x4 word[EL / 2];
+  bool ok = true;
+  for (unsigned polls = 0;;) {
+#pragma unroll
+    for (int m = 0; m < EL / 2; ++m) word[m] = buf_load16<kAuxCoherent>(lr, uint32_t(EL * lane + 2 * m) * 8u);
+    bool ready = true;
+#pragma unroll
+    for (int m = 0; m < EL / 2; ++m) {
+      const int e = EL * lane + 2 * m;
+      ready = ready & (e >= E || word[m].y == tag) & (e + 1 >= E || word[m].w == tag);
+    }
+    if (__all(ready)) break;
+    if (++polls >= kSpinLimit) {
+      ok = false;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  uint32_t key[EL];
+  int kid[EL];
+#pragma unroll
+  for (int m = 0; m < EL / 2; ++m) {
+    const int e = EL * lane + 2 * m;
+    key[2 * m] = (ok && e < E) ? ord_key(__uint_as_float(word[m].x)) : 0u;
+    key[2 * m + 1] = (ok && e + 1 < E) ? ord_key(__uint_as_float(word[m].z)) : 0u;
+    kid[2 * m] = e;
+    kid[2 * m + 1] = e + 1;
+  }
+  // Odd-even transposition sort of the lane's EL keys.
+#pragma unroll
+  for (int r = 0; r < EL; ++r)
+#pragma unroll
+    for (int j = r & 1; j + 1 < EL; j += 2) {
+      const bool sw = key[j + 1] > key[j] || (key[j + 1] == key[j] && kid[j + 1] < kid[j]);
+      const uint32_t k0 = key[j], k1 = key[j + 1];
+      const int i0 = kid[j], i1 = kid[j + 1];
+      key[j] = sw ? k1 : k0;
+      key[j + 1] = sw ? k0 : k1;
+      kid[j] = sw ? i1 : i0;
+      kid[j + 1] = sw ? i0 : i1;
+    }
+  float my_v = 0.f;
+  my_e = 0;
+  for (int s = 0; s < K; ++s) {
+    const uint32_t best = wave_max_u32(key[0]);
+    const unsigned long long m = __ballot(key[0] == best);
+    const int L = m != 0ull ? int(__builtin_ctzll(m)) : 0;
+    const int e = __builtin_amdgcn_readlane(kid[0], L);
+    const bool pop = lane == L;
+#pragma unroll
+    for (int j = 0; j + 1 < EL; ++j) {
+      key[j] = pop ? key[j + 1] : key[j];
+      kid[j] = pop ? kid[j + 1] : kid[j];
+    }
+    key[EL - 1] = pop ? 0u : key[EL - 1];
+    if (lane == s) {
+      my_e = (best != 0u && e < E) ? e : 0;  // 0 = absent (timed-out wait)
+      my_v = ord_value(best);
+    }
+  }
+  // Slot 0 holds the largest logit; exp(v_s - v_0) summed in slot order.
+  const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
+  const float ex = lane < K ? expf(my_v - first) : 0.f;
+  float denom = 0.f;
+  for (int s = 0; s < K; ++s) denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), s));
+  my_w = ex / denom;
+  return ok;
+}
+
 // HC / IC: 16-byte chunks per lane of a hidden-long / intermediate-long row.
 // MB: largest batch of this instantiation (1 = the single-token fast path).
 // EL: router logits held per lane in the top-k (E <= 64*EL).
@@ -253,9 +330,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // window [entries][Ip] and the shared act [B][Isp].
   const int ulimit = min(E, B * K);
   float* xn = reinterpret_cast<float*>(smem);
-  const size_t region_a = size_t(max(B * Hp, kActWindowBytes / 4 + B * Isp));
+  const size_t region_a = size_t(max(B * Hp, a.win_floats + B * Isp));
   float* act_l = xn;
-  float* sact_l = xn + kActWindowBytes / 4;
+  float* sact_l = xn + a.win_floats;
   float* red = xn + region_a;                                        // [kWaves][2*MB]
   float* sgf = red + kWaves * 2 * MB;                             // [MB]
   float* sel_w = sgf + MB;                                        // [MB*K]
@@ -268,6 +345,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   int* ent_of = ent_src + MB * K;                                 // [ulimit][MB] window entry of (u, b)
   int* misc = ent_of + ulimit * MB;                               // [0]=U, [1..kWaves] counts, [16] error
   float* part = reinterpret_cast<float*>(misc + 32);                 // [rows_per_wg][MB] running sums
+  int* ent_base = reinterpret_cast<int*>(part + a.rows_per_wg * MB);  // [ulimit + 1] first entry of expert u
 
   // ---- phase 0 -------------------------------------------------------------
 
@@ -303,8 +381,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   const int nrows = max(0, min(a.rows_per_wg, H - h0));
   // Shared-expert gate/up rows and the shared down row of this wave's first
   // output row are independent of the routing.  The multi-row path fetches
-  // them now; the one-row path only once its router logits are out, so that
-  // the router rows do not queue behind 6 MB of shared-expert rows.
+  // the gate/up rows now; the one-row path only once its router logits are
+  // out, so that the router rows do not queue behind 6 MB of shared-expert
+  // rows.  Both fetch the down row at the end of the gate/up phase (held from
+  // here it would stay live through every phase).
   u32x4 sgr[HC], sur[HC], sdn[IC];
   auto issue_shared_gu = [&]() {
     load_row<T, VEC, HC>(a.sg + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sgr);
@@ -313,10 +393,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   auto issue_shared_down = [&]() {
     load_row<T, VEC, IC>(a.sd + size_t(min(h0 + wave, H - 1)) * Is, Is, wave < nrows, lane, sdn);
   };
-  if constexpr (MB > 1) {
-    issue_shared_gu();
-    issue_shared_down();
-  }
+  if constexpr (MB > 1) issue_shared_gu();
   pin_loads();
 
   if constexpr (MB > 1)
@@ -327,18 +404,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     for (int b = 0; b < MB; ++b) ss[b] = gs[b] = 0.f;
     if constexpr (VEC) {
       // chunk q = (row q / hq, chunk q % hq); the first 4*512 chunks were
-      // loaded above, any beyond (B*H > 16384 elements) are loaded here.
-      for (int q0 = tid; q0 < B * hq; q0 += 4 * kThreads) {
-        if (q0 != tid) {
-          const rsrc_t xr = make_rsrc(a.x, uint32_t(B) * uint32_t(H) * uint32_t(sizeof(T)));
-          const rsrc_t nr = make_rsrc(a.nw, uint32_t(H) * uint32_t(sizeof(T)));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int q = q0 + r * kThreads;
-            xc[r] = buf_load16(xr, q < B * hq ? uint32_t(q) * 16u : 0xFFFFFFF0u);
-            nc[r] = buf_load16(nr, uint32_t(q % hq) * 16u);
-          }
-        }
+      // loaded above and are processed outside the loop (so their waits are
+      // exact), any beyond (B*H > 16384 elements) are loaded in the loop.
+      auto sq_batch = [&](int q0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int q = q0 + r * kThreads;
@@ -360,6 +428,21 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
             for (int bb = 0; bb < MB; ++bb) ss[bb] += bb == b ? sq : 0.f;
           }
         }
+      };
+      sq_batch(tid);
+      // With HC <= 4 (H <= 2048 for 16-bit types) and B <= 8 every chunk is
+      // in the first batch; compiling the loop out keeps the waits exact.
+      if constexpr (HC > 4)
+      for (int q0 = tid + 4 * kThreads; q0 < B * hq; q0 += 4 * kThreads) {
+        const rsrc_t xr = make_rsrc(a.x, uint32_t(B) * uint32_t(H) * uint32_t(sizeof(T)));
+        const rsrc_t nr = make_rsrc(a.nw, uint32_t(H) * uint32_t(sizeof(T)));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int q = q0 + r * kThreads;
+          xc[r] = buf_load16(xr, q < B * hq ? uint32_t(q) * 16u : 0xFFFFFFF0u);
+          nc[r] = buf_load16(nr, uint32_t(q % hq) * 16u);
+        }
+        sq_batch(q0);
       }
     } else {
       for (int h = tid; h < Hp; h += kThreads) {
@@ -389,11 +472,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     }
     // Scale to x_norm in place; dot with the shared-expert gate vector.
     if constexpr (VEC) {
-      for (int q0 = tid; q0 < B * hq; q0 += 4 * kThreads) {
-        if (q0 != tid) {  // the first 4*512 chunks' gate vector was loaded at the start
-#pragma unroll
-          for (int r = 0; r < 4; ++r) gc[r] = buf_load16(gsr, uint32_t((q0 + r * kThreads) % hq) * 16u);
-        }
+      auto scale_batch = [&](int q0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int q = q0 + r * kThreads;
@@ -423,6 +502,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
             for (int bb = 0; bb < MB; ++bb) gs[bb] += bb == b ? dg : 0.f;
           }
         }
+      };
+      scale_batch(tid);  // the first 4*512 chunks' gate vector was loaded at the start
+      if constexpr (HC > 4)
+      for (int q0 = tid + 4 * kThreads; q0 < B * hq; q0 += 4 * kThreads) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gc[r] = buf_load16(gsr, uint32_t((q0 + r * kThreads) % hq) * 16u);
+        scale_batch(q0);
       }
     } else {
       for (int h = tid; h < Hp; h += kThreads) {
@@ -497,74 +583,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     // Lane s keeps slot s (expert, logit); the softmax over the K selected
     // logits is taken once at the end, all slots in parallel.
     if (wave == 0) {
-      const rsrc_t lr = make_rsrc(w.logits, uint32_t(E) * 8u);
-      u32x4 word[EL / 2];
-      bool ok = true;
-      for (unsigned polls = 0;;) {
-#pragma unroll
-        for (int m = 0; m < EL / 2; ++m) word[m] = buf_load16<kAuxCoherent>(lr, uint32_t(EL * lane + 2 * m) * 8u);
-        bool ready = true;
-#pragma unroll
-        for (int m = 0; m < EL / 2; ++m) {
-          const int e = EL * lane + 2 * m;
-          ready = ready & (e >= E || word[m].y == tag) & (e + 1 >= E || word[m].w == tag);
-        }
-        if (__all(ready)) break;
-        if (++polls >= kSpinLimit) {
-          ok = false;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      if (!ok && lane == 0) misc[16] = 1;
-      uint32_t key[EL];
-      int kid[EL];
-#pragma unroll
-      for (int m = 0; m < EL / 2; ++m) {
-        const int e = EL * lane + 2 * m;
-        key[2 * m] = (ok && e < E) ? ord_key(__uint_as_float(word[m].x)) : 0u;
-        key[2 * m + 1] = (ok && e + 1 < E) ? ord_key(__uint_as_float(word[m].z)) : 0u;
-        kid[2 * m] = e;
-        kid[2 * m + 1] = e + 1;
-      }
-      // Odd-even transposition sort of the lane's EL keys.
-#pragma unroll
-      for (int r = 0; r < EL; ++r)
-#pragma unroll
-        for (int j = r & 1; j + 1 < EL; j += 2) {
-          const bool sw = key[j + 1] > key[j] || (key[j + 1] == key[j] && kid[j + 1] < kid[j]);
-          const uint32_t k0 = key[j], k1 = key[j + 1];
-          const int i0 = kid[j], i1 = kid[j + 1];
-          key[j] = sw ? k1 : k0;
-          key[j + 1] = sw ? k0 : k1;
-          kid[j] = sw ? i1 : i0;
-          kid[j + 1] = sw ? i0 : i1;
-        }
-      float my_v = 0.f;
-      int my_e = 0;
-      for (int s = 0; s < K; ++s) {
-        const uint32_t best = wave_max_u32(key[0]);
-        const unsigned long long m = __ballot(key[0] == best);
-        const int L = m != 0ull ? int(__builtin_ctzll(m)) : 0;
-        const int e = __builtin_amdgcn_readlane(kid[0], L);
-        const bool pop = lane == L;
-#pragma unroll
-        for (int j = 0; j + 1 < EL; ++j) {
-          key[j] = pop ? key[j + 1] : key[j];
-          kid[j] = pop ? kid[j + 1] : kid[j];
-        }
-        key[EL - 1] = pop ? 0u : key[EL - 1];
-        if (lane == s) {
-          my_e = (best != 0u && e < E) ? e : 0;  // 0 = absent (timed-out wait)
-          my_v = ord_value(best);
-        }
-      }
-      // Slot 0 holds the largest logit; exp(v_s - v_0) summed in slot order.
-      const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
-      const float ex = lane < K ? expf(my_v - first) : 0.f;
-      float denom = 0.f;
-      for (int s = 0; s < K; ++s) denom += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), s));
-      const float my_w = ex / denom;
+      int my_e;
+      float my_w;
+      if (!route_row<EL>(make_rsrc(w.logits, uint32_t(E) * 8u), E, K, tag, lane, my_e, my_w) && lane == 0)
+        misc[16] = 1;
       if (lane < K) {
         sel_e[lane] = my_e;
         sel_w[lane] = my_w;
@@ -720,66 +742,17 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   } else {
 
   // ---- phase 1: gather the router logits, top-k -----------------------------
+  // Wave b routes batch row b.
   if (wave < B) {
     const int b = wave;
-    const rsrc_t lr = make_rsrc(w.logits + size_t(b) * E, uint32_t(E) * 8u);
-    u32x2 word[EL];
-    unsigned polls = 0;
-    bool ok = true;
-    while (true) {
-#pragma unroll
-      for (int j = 0; j < EL; ++j) word[j] = ld8_coherent(lr, uint32_t(lane + kWave * j) * 8u);
-      bool ready = true;
-#pragma unroll
-      for (int j = 0; j < EL; ++j) ready = ready & (lane + kWave * j >= E || word[j].y == tag);
-      if (__all(ready)) break;
-      if (++polls >= kSpinLimit) {
-        ok = false;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (!ok && lane == 0) {
+    int my_e;
+    float my_w;
+    if (!route_row<EL>(make_rsrc(w.logits + size_t(b) * E, uint32_t(E) * 8u), E, K, tag, lane, my_e, my_w) &&
+        lane == 0) {
       misc[16] = 1;
       __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // Top-k: K rounds of a wave-wide max over order-preserving 32-bit keys of
-    // the logits (0 = absent/taken).  The winner's index is the lowest index
-    // holding the max key (ballot per key slot, slots in index order), which
-    // is the reference's tie rule.  Lane s keeps slot s.
-    uint32_t key[EL];
-#pragma unroll
-    for (int j = 0; j < EL; ++j) {
-      const int e = lane + kWave * j;
-      key[j] = (ok && e < E) ? ord_key(__uint_as_float(word[j].x)) : 0u;
-    }
-    float first = 0.f, denom = 0.f, my_w = 0.f;
-    int my_e = 0;
-    for (int s = 0; s < K; ++s) {
-      uint32_t lk = key[0];
-#pragma unroll
-      for (int j = 1; j < EL; ++j) lk = max(lk, key[j]);
-      const uint32_t best = wave_max_u32(lk);
-      // lowest index holding `best`: last matching slot wins going downward
-      int bi = -1;
-#pragma unroll
-      for (int j = EL - 1; j >= 0; --j) {
-        const unsigned long long m = __ballot(key[j] == best);
-        bi = m != 0ull ? kWave * j + int(__builtin_ctzll(m)) : bi;
-      }
-#pragma unroll
-      for (int j = 0; j < EL; ++j) key[j] = (kWave * j + lane == bi) ? 0u : key[j];
-      const float bv = ord_value(best);
-      if (s == 0) first = bv;
-      const float ex = expf(bv - first);
-      denom += ex;
-      if (lane == s) {
-        my_e = (bi >= 0 && bi < E) ? bi : 0;
-        my_w = ex;
-      }
-    }
     if (lane < K) {
-      my_w /= denom;
       sel_e[b * K + lane] = my_e;
       sel_w[b * K + lane] = my_w;
       if constexpr (MB > 1) atomicOr(&emask[my_e], 1u << b);
@@ -837,6 +810,34 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     uslot[t] = slot;
   }
   __syncthreads();
+  // Act entries (u, b) in expert order, then batch-row order: entry of
+  // (u, b) = ent_base[u] + rank of b among expert u's rows.  The prefix sum
+  // over the experts' row counts runs in one wave; the table is filled by all.
+  if (wave == 0) {
+    int carry = 0;
+    for (int u0 = 0; u0 < U; u0 += kWave) {
+      const int u = u0 + lane;
+      int c = u < U ? __popc(umask[u]) : 0;
+      for (int d = 1; d < kWave; d <<= 1) {
+        const int v = __shfl_up(c, d, kWave);
+        c += lane >= d ? v : 0;
+      }
+      if (u < U) ent_base[u + 1] = carry + c;
+      carry += __shfl(c, kWave - 1, kWave);
+    }
+    if (lane == 0) ent_base[0] = 0;
+  }
+  __syncthreads();
+  for (int t = tid; t < U * MB; t += kThreads) {
+    const int u = t / MB, b = t % MB;
+    const unsigned m = umask[u];
+    if ((m >> b) & 1u) {
+      const int en = ent_base[u] + __popc(m & ((1u << b) - 1u));
+      ent_src[en] = b * K + uslot[t];
+      ent_of[t] = en;
+    }
+  }
+  __syncthreads();
 
   // ---- phase 2: routed gate/up (+ early issue of the down rows) -------------
   const int nw_total = nwg * kWaves;
@@ -848,10 +849,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // Loads complete in issue order, so the first gate/up group is issued before
   // the down rows: act is published as soon as its own rows arrive, while the
   // down rows keep streaming during the hand-off.
-  const int step = nw_total * kGU;
-  auto issue_gu = [&](int t0, u32x4 (&g)[kGU][HC], u32x4 (&u)[kGU][HC]) {
+  const int step = nw_total * kGUM;
+  auto issue_gu = [&](int t0, u32x4 (&g)[kGUM][HC], u32x4 (&u)[kGUM][HC]) {
 #pragma unroll
-    for (int q = 0; q < kGU; ++q) {
+    for (int q = 0; q < kGUM; ++q) {
       const int t = t0 + q * nw_total;
       const int tc = min(t, ntask - 1);
       const size_t ro = (size_t(ulist[tc / I]) * I + tc % I) * H;
@@ -859,9 +860,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       load_row<T, VEC, HC>(a.eu + ro, H, t < ntask, lane, u[q]);
     }
   };
-  auto compute_gu = [&](int t0, const u32x4 (&g)[kGU][HC], const u32x4 (&u)[kGU][HC]) {
+  auto compute_gu = [&](int t0, const u32x4 (&g)[kGUM][HC], const u32x4 (&u)[kGUM][HC]) {
 #pragma unroll
-    for (int q = 0; q < kGU; ++q) {
+    for (int q = 0; q < kGUM; ++q) {
       const int t = t0 + q * nw_total;
       if (t < ntask) {
         const int ue = t / I, i = t % I;
@@ -879,16 +880,17 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       }
     }
   };
-  u32x4 gA[kGU][HC], uA[kGU][HC], gB[kGU][HC], uB[kGU][HC];
+  u32x4 gA[kGUM][HC], uA[kGUM][HC], gB[kGUM][HC], uB[kGUM][HC];
   issue_gu(gw, gA, uA);
 
   // Double-buffered: the next group is in flight while this one is reduced.
+  // Groups are issued unconditionally (tasks past ntask are zero-size loads),
+  // so the waits before a group's use cover only that group.
   for (int t0 = gw; t0 < ntask; t0 += 2 * step) {
-    if (t0 + step < ntask) issue_gu(t0 + step, gB, uB);
+    issue_gu(t0 + step, gB, uB);
     pin_loads();
     compute_gu(t0, gA, uA);
-    if (t0 + step >= ntask) break;
-    if (t0 + 2 * step < ntask) issue_gu(t0 + 2 * step, gA, uA);
+    issue_gu(t0 + 2 * step, gA, uA);
     pin_loads();
     compute_gu(t0 + step, gB, uB);
   }
@@ -900,6 +902,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   for (int j = 0; j < kDN; ++j)
     load_row<T, VEC, IC>(a.ed + (size_t(ulist[min(j, U - 1)]) * H + min(h0 + wave, H - 1)) * I, I,
                          j < U && wave < nrows, lane, dn[j]);
+  issue_shared_down();
   pin_loads();
   __syncthreads();  // x_norm (region A) is dead from here on
 
@@ -939,26 +942,15 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // the residual and writes the row.  The down rows of (hl = w, expert u < kDN)
   // were issued in phase 2.
   for (int t = tid; t < a.rows_per_wg * MB; t += kThreads) part[t] = 0.f;
-  const int win_entries = max(1, (kActWindowBytes / 4) / Ip);
+  // Windows of whole experts, at most win_entries act rows each (the host
+  // sizes the window for at least kMaxB rows, one expert's worst case).
+  const int win_entries = a.win_floats / Ip;
   int u_lo = 0;
   while (u_lo < U) {
-    int u_hi = u_lo, ent = 0;
-    while (u_hi < U && (ent + __popc(umask[u_hi]) <= win_entries || u_hi == u_lo)) {
-      ent += __popc(umask[u_hi]);
-      ++u_hi;
-    }
+    int u_hi = u_lo + 1;
+    while (u_hi < U && ent_base[u_hi + 1] - ent_base[u_lo] <= win_entries) ++u_hi;
+    const int e_lo = ent_base[u_lo], ent = ent_base[u_hi] - e_lo;
     __syncthreads();  // previous window fully consumed
-    if (tid == 0) {
-      int en = 0;
-      for (int u = u_lo; u < u_hi; ++u)
-        for (int b = 0; b < MB; ++b)
-          if ((umask[u] >> b) & 1u) {
-            ent_src[en] = b * K + uslot[u * MB + b];
-            ent_of[u * MB + b] = en;
-            ++en;
-          }
-    }
-    __syncthreads();
     if constexpr (VEC) {
       const rsrc_t ar = make_rsrc(w.act, uint32_t(B) * uint32_t(K) * uint32_t(I) * 8u);
       const int hp = Ip / 2;
@@ -966,7 +958,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
                 ar, ent * hp,
                 [&](int f) -> uint32_t {
                   const int en = f / hp, c2 = (f % hp) * 2;
-                  return c2 < I ? uint32_t(ent_src[en] * I + c2) * 8u : 0xFFFFFFF0u;
+                  return c2 < I ? uint32_t(ent_src[e_lo + en] * I + c2) * 8u : 0xFFFFFFF0u;
                 },
                 act_l, tag, tid) &&
             ok3;
@@ -976,7 +968,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         float val = 0.f;
         if (i < I) {
           uint64_t word = 0;
-          const uint64_t* pw = w.act + size_t(ent_src[en]) * I + i;
+          const uint64_t* pw = w.act + size_t(ent_src[e_lo + en]) * I + i;
           for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
             word = __hip_atomic_load(const_cast<uint64_t*>(pw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (unsigned(word >> 32) == tag) break;
@@ -991,18 +983,20 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     if (!ok3) misc[16] = 1;
     __syncthreads();
     for (int hl = wave; hl < nrows; hl += kWaves) {
-      float acc[MB];
+      // Lane partials over this window's experts; one wave reduction per
+      // batch row at the end of the window.
+      float accl[MB];
 #pragma unroll
-      for (int b = 0; b < MB; ++b) acc[b] = part[hl * MB + b];
+      for (int b = 0; b < MB; ++b) accl[b] = 0.f;
       auto add_expert = [&](int u, const u32x4 (&c)[IC]) {
         if constexpr (MB == 1) {  // one row: expert u's act is window entry u - u_lo
-          acc[0] += wave_sum_u(dot_row<T, IC>(c, act_l + size_t(u - u_lo) * Ip, I, lane));
+          accl[0] += dot_row<T, IC>(c, act_l + size_t(u - u_lo) * Ip, I, lane);
         } else {
           const unsigned mask = umask[u];
 #pragma unroll
           for (int b = 0; b < MB; ++b)
             if ((mask >> b) & 1u)
-              acc[b] += wave_sum_u(dot_row<T, IC>(c, act_l + size_t(ent_of[u * MB + b]) * Ip, I, lane));
+              accl[b] += dot_row<T, IC>(c, act_l + size_t(ent_of[u * MB + b] - e_lo) * Ip, I, lane);
         }
       };
       int u_next = u_lo;
@@ -1012,14 +1006,40 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
           if (uu >= u_lo && uu < u_hi) add_expert(uu, dn[uu]);
         u_next = max(u_lo, kDN);
       }
-      for (int u = u_next; u < u_hi; ++u) {
-        u32x4 c[IC];
-        load_row<T, VEC, IC>(a.ed + (size_t(ulist[u]) * H + h0 + hl) * I, I, true, lane, c);
-        add_expert(u, c);
-      }
-      if (lane == 0) {
+      // The remaining down rows stream in groups of kDS, two groups in flight:
+      // the next group is issued before the current one is consumed.  Groups
+      // are issued unconditionally (rows past u_hi are zero-size loads), so
+      // the waits before a group's use cover only that group.
+      const size_t rowoff = size_t(h0 + hl) * I;
+      auto issue_ds = [&](int ub, u32x4 (&c)[kDS][IC]) {
 #pragma unroll
-        for (int b = 0; b < MB; ++b) part[hl * MB + b] = acc[b];
+        for (int j = 0; j < kDS; ++j) {
+          const int u = ub + j;
+          load_row<T, VEC, IC>(a.ed + size_t(ulist[min(u, U - 1)]) * H * I + rowoff, I, u < u_hi, lane, c[j]);
+        }
+      };
+      auto consume_ds = [&](int ub, const u32x4 (&c)[kDS][IC]) {
+#pragma unroll
+        for (int j = 0; j < kDS; ++j)
+          if (ub + j < u_hi) add_expert(ub + j, c[j]);
+      };
+      if (u_next < u_hi) {
+        u32x4 da[kDS][IC], db[kDS][IC];
+        issue_ds(u_next, da);
+        pin_loads();
+        for (int ub = u_next; ub < u_hi; ub += 2 * kDS) {
+          issue_ds(ub + kDS, db);
+          pin_loads();
+          consume_ds(ub, da);
+          issue_ds(ub + 2 * kDS, da);
+          pin_loads();
+          consume_ds(ub + kDS, db);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        const float t = wave_sum_u(accl[b]);
+        if (lane == 0) part[hl * MB + b] += t;
       }
     }
     u_lo = u_hi;
@@ -1068,17 +1088,15 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   }
 }
 
-size_t lds_bytes(int B, int H, int E, int I, int Is, int K, int epc, int rows_per_wg) {
-  const int Hp = round_up(H, epc), Isp = round_up(Is, epc);
-  const int ulimit = E < B * K ? E : B * K;
-  size_t region_a = size_t(B) * Hp;
-  const size_t r3 = size_t(kActWindowBytes / 4) + size_t(B) * Isp;
-  if (r3 > region_a) region_a = r3;
-  size_t n = region_a + kWaves * 2 * kMaxB + kMaxB + kMaxB * K;                    // floats
+// LDS floats besides region A (x_norm, later the act window and shared act),
+// for kMaxB rows.
+size_t lds_fixed_floats(int E, int K, int rows_per_wg) {
+  const int ulimit = E < kMaxB * K ? E : kMaxB * K;
+  size_t n = kWaves * 2 * kMaxB + kMaxB + kMaxB * K;                                            // floats
   n += kMaxB * K + E + ulimit + ulimit + size_t(ulimit) * kMaxB + kMaxB * K + size_t(ulimit) * kMaxB + 32;  // ints
-  n += size_t(rows_per_wg) * kMaxB;
-  (void)I;
-  return n * 4;
+  n += size_t(rows_per_wg) * kMaxB;  // part
+  n += size_t(ulimit) + 1;           // ent_base
+  return n;
 }
 
 template <typename T>
@@ -1092,18 +1110,29 @@ int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
   const bool vec = (a.H % EPC == 0) && (a.I % EPC == 0) && (a.Is % EPC == 0) && aligned16(a.x) &&
                    aligned16(a.nw) && aligned16(a.router) && aligned16(a.eg) && aligned16(a.eu) && aligned16(a.ed) &&
                    aligned16(a.sg) && aligned16(a.su) && aligned16(a.sd) && (a.wsg == nullptr || aligned16(a.wsg));
-  const size_t lds = lds_bytes(kMaxB, a.H, a.E, a.I, a.Is, a.K, EPC, a.rows_per_wg);
-  if (lds > size_t(max_lds_per_block()))
-    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: shape needs %zu bytes of LDS (> %d)", lds, max_lds_per_block());
+  // Region A holds x_norm [kMaxB][Hp], later the act window and the shared act
+  // [kMaxB][Isp].  The window takes what the LDS leaves, up to every act row
+  // of the launch (B * K rows of Ip), and at least kMaxB rows (one expert's
+  // rows of every batch row).
+  const size_t Hp = round_up(a.H, EPC), Ip = round_up(a.I, EPC), Isp = round_up(a.Is, EPC);
+  const size_t fixed = lds_fixed_floats(a.E, a.K, a.rows_per_wg);
+  const size_t limit = size_t(max_lds_per_block()) / 4;
+  const size_t avail = limit > fixed ? limit - fixed : 0;
+  const size_t want = size_t(kMaxB) * a.K * Ip;
+  const size_t room = avail > size_t(kMaxB) * Isp ? avail - size_t(kMaxB) * Isp : 0;
+  const size_t win = (room < want ? room : want) / Ip * Ip;
+  if (avail < size_t(kMaxB) * Hp || win < size_t(kMaxB) * Ip)
+    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: shape does not fit the %zu bytes of LDS", limit * 4);
+  a.win_floats = int(win);
+  const size_t region_floats = max(size_t(kMaxB) * Hp, win + size_t(kMaxB) * Isp);
+  const size_t lds = 4 * (fixed + region_floats);
   // Chunk counts per lane: the smallest instantiation that covers the rows.
   const int hc_need = (a.H + EPC * kWave - 1) / (EPC * kWave);
   const int ic_need = (max(a.I, a.Is) + EPC * kWave - 1) / (EPC * kWave);
   // The one-row path keeps x_norm, act [K][Ip] and the shared act side by side
   // in the LDS region that the multi-row path shares between them.
-  const size_t one_row_floats = size_t(round_up(a.H, EPC)) + size_t(a.K) * round_up(a.I, EPC) + round_up(a.Is, EPC);
-  const size_t region_floats = max(size_t(kMaxB) * round_up(a.H, EPC),
-                                   size_t(kActWindowBytes / 4) + size_t(kMaxB) * round_up(a.Is, EPC));
-  const bool one_row_ok = batch == 1 && one_row_floats <= region_floats;
+  const size_t one_row_floats = Hp + size_t(a.K) * Ip + Isp;
+  const bool one_row_ok = batch == 1 && one_row_floats <= max(Hp, win + Isp);  // region A as sized for B = 1
   const int which = (vec && hc_need <= 4 && ic_need <= 1) ? (one_row_ok ? 0 : 1) : (vec ? 2 : 3);
   const bool el4 = a.E <= 4 * kWave;
   void (*kern)(MoeArgs<T>) = which == 0   ? (el4 ? &moe_decode_kernel<T, true, 4, 1, 1, 4>
