@@ -11,10 +11,11 @@
 // Workgroups of the same chunk for consecutive units are adjacent in launch
 // order, so the kv heads stored side by side in one token row are read
 // together.  Per tile a wave
-//   * holds the K tile in MFMA A-operand registers (16 tokens x 32 dims per
-//     v_mfma_f32_16x16x32, 16 bytes per lane) and computes S^T = K Q^T for all
-//     q heads of the group at once -- the G q heads of a kv head reuse one read
-//     of K and V;
+//   * loads the K tile as two 512-byte token rows per instruction (full cache
+//     lines; the A-operand layout would take 16 tokens x 64 bytes), stages it
+//     in wave-private LDS and reads it back as MFMA A operands (16 tokens x 32
+//     dims per v_mfma_f32_16x16x32), computing S^T = K Q^T for all q heads of
+//     the group at once -- the G q heads of a kv head reuse one read of K and V;
 //   * runs an online softmax in the base-2 domain; the probabilities stay in
 //     the registers of the S^T result, whose layout (lane (head c, group g)
 //     holds tokens 4g..4g+3) is exactly the B operand of v_mfma_f32_16x16x16;
@@ -80,6 +81,13 @@ struct Mfma<f16_t> {
 // 2 mod 8 dwords, so the four token rows 4g+j (g = 0..3) that one transposed
 // read touches start 8 banks apart and cover 32 distinct banks.
 constexpr __host__ __device__ int v_stride(int d) { return 2 * (d / 2 + ((2 - d / 2) % 8 + 8) % 8); }
+// LDS row stride (bytes) of a staged K tile: D * 2 + 16, so the 16-byte A
+// operand reads of 8 consecutive tokens start 4 banks apart (conflict free).
+constexpr __host__ __device__ int k_stride_bytes(int d) { return 2 * d + 16; }
+// Staging bytes per wave: the K tile and then the V tile use the same area.
+constexpr __host__ __device__ int stage_bytes(int d) {
+  return kTT * (k_stride_bytes(d) > 2 * v_stride(d) ? k_stride_bytes(d) : 2 * v_stride(d));
+}
 
 // Row stride (floats) of a wave's O block in the merge area.
 __host__ __device__ inline int o_stride(int d) { return d + 4; }
@@ -88,7 +96,7 @@ __host__ __device__ inline size_t merge_floats(int d, int heads) { return size_t
 
 template <int DT>
 size_t chunk_lds_bytes(int d, int heads) {
-  const size_t stage = size_t(kWaves) * kTT * v_stride(DT) * 2;
+  const size_t stage = size_t(kWaves) * stage_bytes(DT);
   const size_t merge = size_t(kWaves) * merge_floats(d, heads) * 4;
   return stage > merge ? stage : merge;
 }
@@ -131,14 +139,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   // heads past the group read zero.
   const rsrc_t qr = make_rsrc(q + (size_t(b) * hq + qh0) * d, uint32_t(heads_here * d * sizeof(T)));
   V8 qop[NS];
-  uint32_t koff[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int d0 = 32 * s + 8 * grp;
-    koff[s] = d0 < d ? uint32_t(d0 * sizeof(T)) : kFar;
-    qop[s] = __builtin_bit_cast(V8, buf_load16(qr, uint32_t(col * d * sizeof(T)) + koff[s]));
+    qop[s] = __builtin_bit_cast(V8, buf_load16(qr, d0 < d ? uint32_t(col * d + d0) * uint32_t(sizeof(T)) : kFar));
   }
-  // V chunk i of a tile: token row qi / CPR, dims 8 * (qi % CPR), qi = lane + 64 i.
+  // K and V chunk i of a tile: token row qi / CPR, dims 8 * (qi % CPR),
+  // qi = lane + 64 i (two 512-byte token rows per load at D = 256).
   uint32_t voff[VCH];
 #pragma unroll
   for (int i = 0; i < VCH; ++i) {
@@ -146,31 +153,42 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const int row = qi / CPR, dc = qi % CPR;
     voff[i] = uint32_t(row) * tsb + (dc * 8 < d ? uint32_t(dc * 16) : kFar);
   }
-  uint16_t* vt = reinterpret_cast<uint16_t*>(smem) + size_t(wave) * kTT * VSTR;
+  unsigned char* stage = smem + size_t(wave) * stage_bytes(DT);
+  uint16_t* vt = reinterpret_cast<uint16_t*>(stage);
+  constexpr int KSTR = k_stride_bytes(DT);
 
   f32x4 oacc[NDT];
 #pragma unroll
   for (int n = 0; n < NDT; ++n) oacc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegInf, l_run = 0.f;
 
-  u32x4 kreg[NS], vreg[VCH];
+  u32x4 kreg[VCH], vreg[VCH];
   int t0 = wave * kTT;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) kreg[s] = buf_load16<kAuxStream>(kr, uint32_t(t0 + col) * tsb + koff[s]);
+  for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(kr, uint32_t(t0) * tsb + voff[i]);
 #pragma unroll
   for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, uint32_t(t0) * tsb + voff[i]);
   pin_loads();
 
   const int ntiles = len > t0 ? (len - t0 + kWgTokens - 1) / kWgTokens : 0;
   for (int it = 0; it < ntiles; ++it, t0 += kWgTokens) {
-    // S^T = K Q^T: sacc[i] = score(token t0 + 4grp + i, head col).
-    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Stage K, then S^T = K Q^T: sacc[i] = score(token t0 + 4grp + i, head col);
+    // lane (token col, grp) reads dims 32 s + 8 grp of its token row.
 #pragma unroll
-    for (int s = 0; s < NS; ++s) sacc = Mfma<T>::qk(__builtin_bit_cast(V8, kreg[s]), qop[s], sacc);
+    for (int i = 0; i < VCH; ++i) {
+      const int qi = lane + kWave * i;
+      *reinterpret_cast<u32x4*>(stage + (qi / CPR) * KSTR + (qi % CPR) * 16) = kreg[i];
+    }
     const uint32_t next = uint32_t(t0 + kWgTokens) * tsb;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) kreg[s] = buf_load16<kAuxStream>(kr, next + uint32_t(col) * tsb + koff[s]);
+    for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(kr, next + voff[i]);
     pin_loads();
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const u32x4 ka = *reinterpret_cast<const u32x4*>(stage + col * KSTR + (32 * s + 8 * grp) * 2);
+      sacc = Mfma<T>::qk(__builtin_bit_cast(V8, ka), qop[s], sacc);
+    }
 
     // Online softmax (base 2); m is kept equal across the 4 lanes of a head.
     float sv[4];
