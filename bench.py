@@ -68,6 +68,20 @@ def linear_bytes(batch, k_heads, v_heads, dk, dv, elt=2):
     return batch * (2 * v_heads * dk * dv * 4 + 2 * k_heads * dk * elt + 2 * v_heads * dv * elt + 2 * v_heads * 4)
 
 
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (copy-calibrated), or None."""
+    try:
+        with open(REPO / "profiles" / "hbm_traffic_counters.md") as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 4 and parts[:3] == ["traffic", kernel, workload]:
+                    return int(parts[3])
+    except OSError:
+        pass
+    return None
+
+
 # ---------------------------------------------------------------------------
 # GPU timing
 # ---------------------------------------------------------------------------
@@ -200,6 +214,68 @@ def bench_linear(mk, inputs, timer, steps, warmup, batches):
     return out
 
 
+def bench_layer(mk, inputs, timer, steps, warmup, batches):
+    """decode_layer at layer 0 (linear attention): config 5's gated delta rule
+    with an out_proj [2048, 32*128] onto the hidden size, then the config-2 MoE."""
+    import dataclasses
+
+    import torch
+
+    out = {}
+    for b in batches:
+        x, w, k = inputs.make_moe(batch=b)
+        lin = inputs.make_gated_delta(batch=b)
+        g = torch.Generator().manual_seed(999)
+        proj = (torch.randn(2048, 32 * 128, generator=g) * 0.02).to("cuda", torch.bfloat16)
+        lin = dataclasses.replace(lin, out_proj=proj)
+        res = mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+        distinct = int(torch.unique(res.router_indices).numel())
+        nbytes = (linear_bytes(b, 16, 32, 128, 128) + proj.numel() * 2
+                  + moe_bytes(b, 2048, 256, 512, 512, k, distinct))
+        fn = lambda: mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)  # noqa: E731
+        cold = with_bw(timer.run(fn, steps, warmup, cold=True), nbytes)
+        cold["warm_median_us"] = timer.run(fn, steps, warmup, cold=False)["median_us"]
+        out[f"layer_linear_moe_b{b}"] = cold
+        log(f"decode_layer (gated delta + out_proj + MoE) b={b}: {cold['median_us']:.2f} us cold "
+            f"({cold['gbps']:.0f} GB/s), {cold['warm_median_us']:.2f} us warm")
+        del x, w, lin
+        torch.cuda.empty_cache()
+    return out
+
+
+def pmc_workload(mk, inputs, name, launches=10):
+    """Runs one op (or a plain copy of known size) `launches` times, each after
+    the cache flush, for rocprofv3 counter passes; prints no JSON line."""
+    import torch
+
+    flush = torch.zeros((1 << 30) // 4, dtype=torch.float32, device="cuda")
+    if name == "copy":
+        src = torch.ones((256 << 20) // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        fn = lambda: dst.copy_(src)  # noqa: E731
+    elif name == "moe":
+        x, w, k = inputs.make_moe(batch=1)
+        fn = lambda: mk.moe_decode(x, w, top_k=k)  # noqa: E731
+    elif name == "dense":
+        x, w = inputs.make_dense(batch=1)
+        fn = lambda: mk.dense_ffn_decode(x, w)  # noqa: E731
+    elif name == "attn":
+        inp = inputs.make_attention(seq_len=32768)
+        fn = lambda: mk.full_attention_decode(inp)  # noqa: E731
+    elif name == "linear":
+        inp = inputs.make_gated_delta(batch=1)
+        fn = lambda: mk.linear_attention_decode(inp)  # noqa: E731
+    else:
+        raise SystemExit(f"unknown --pmc-workload {name}")
+    fn()
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        flush.sum()
+        fn()
+    torch.cuda.synchronize()
+    log(f"pmc workload {name}: {launches} launches done")
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline (oracle = numpy restatement of reference.py, on host cores)
 # ---------------------------------------------------------------------------
@@ -256,7 +332,9 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--ops", default="moe,dense,attn,linear")
+    ap.add_argument("--ops", default="moe,dense,attn,linear,layer")
+    ap.add_argument("--pmc-workload", choices=("moe", "dense", "attn", "linear", "copy"), default=None,
+                    help="run one op (or a 256 MiB copy) 10 times after flushes for a rocprofv3 --pmc pass; no JSON")
     ap.add_argument("--quick", action="store_true", help="batch 1 / 32K only")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
@@ -281,6 +359,9 @@ def main(argv=None):
     dev = torch.cuda.get_device_properties(0)
     log(f"device {dev.name} {getattr(dev, 'gcnArchName', '')} CUs={dev.multi_processor_count}")
 
+    if args.pmc_workload:
+        pmc_workload(mk, inputs, args.pmc_workload)
+        return
     timer = Timer(torch, mode=args.flush)
     ops = set(args.ops.split(","))
     results = {}
@@ -294,6 +375,8 @@ def main(argv=None):
                                        [32768] if args.quick else [4096, 32768, 131072]))
     if "linear" in ops:
         results.update(bench_linear(mk, inputs, timer, args.steps, args.warmup, [1] if args.quick else [1, 8]))
+    if "layer" in ops:
+        results.update(bench_layer(mk, inputs, timer, args.steps, args.warmup, [1] if args.quick else [1, 8]))
     gpu_wall = time.perf_counter() - t_start
 
     head = results.get("moe_b1")
@@ -306,7 +389,9 @@ def main(argv=None):
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": head["gbps"] * 1e9 / HBM_PEAK,
-            "traffic": None,
+            "traffic": measured_traffic("moe_decode_kernel", "config2_b1"),
+            "traffic_source": "profiles/hbm_traffic_counters.md (rocprofv3 FETCH_SIZE and WRITE_SIZE passes, "
+                              "scaled by a 256 MiB copy)",
             "kernel": "moe_decode_kernel",
             "bytes_per_launch": head["algorithmic_bytes"],
         }

@@ -1,0 +1,100 @@
+"""GPU parity: decode_layer (reference ops.py:701-748) composed from the HIP ops,
+against the oracle's restatement of the same composition.
+
+Config 5 (gated delta rule: 16 q/k heads, 32 v heads of dim 128) and the GQA
+attention of config 4 feed the config-2 MoE (35B-A3B shape) or a dense FFN,
+with an ``out_proj`` onto the hidden size.  The oracle rounds each op's output
+to bfloat16 before the next op, as the device path does.
+
+Tolerances (task): bf16 outputs atol/rtol 1e-2, FP32 recurrent state 1e-4,
+top-k indices bit-exact.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+import mega_kernel_qwen36 as mk
+import oracle
+from tests.inputs import (assert_close_out, assert_close_state, make_attention, make_dense, make_gated_delta,
+                          make_moe, np32)
+
+pytestmark = pytest.mark.gpu
+
+MOE_FIELDS = ("norm_weight", "router_weight", "expert_gate", "expert_up", "expert_down", "shared_gate", "shared_up",
+              "shared_down", "shared_expert_gate")
+DENSE_FIELDS = ("norm_weight", "gate_weight", "up_weight", "down_weight")
+
+
+def _proj(out_features, in_features, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(out_features, in_features, generator=g) * 0.02).to("cuda", torch.bfloat16)
+
+
+def _np_fields(obj, names):
+    return {n: np32(getattr(obj, n)) for n in names if getattr(obj, n, None) is not None}
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_decode_layer_gated_delta_with_moe(batch):
+    """Config 5 composed with the config-2 MoE (layer 0 is a linear-attention layer)."""
+    x, w, k = make_moe(batch=batch, seed=60 + batch)
+    lin = make_gated_delta(batch=batch, seed=70 + batch)
+    lin = dataclasses.replace(lin, out_proj=_proj(x.shape[1], 32 * 128, 80 + batch))
+    state_before = lin.state.clone()
+    res = mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+    ref = oracle.decode_layer(
+        np32(x), kind="linear_attention", moe=_np_fields(w, MOE_FIELDS), top_k=k,
+        linear_attention=dict(q=np32(lin.q), k=np32(lin.k), v=np32(lin.v), state=np32(lin.state), g=np32(lin.g),
+                              beta=np32(lin.beta), out_proj=np32(lin.out_proj)))
+    assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
+    assert_close_out(res.linear_output, ref["linear_output"])
+    assert_close_state(res.linear_state, ref["linear_state"])
+    assert_close_out(res.hidden, ref["hidden"])
+    assert torch.equal(lin.state, state_before)  # the layer returns a new state
+
+
+def test_decode_layer_full_attention_with_moe():
+    """Layer 3 is a full-attention layer: config-4 GQA (T = 4096) then the MoE."""
+    x, w, k = make_moe(batch=1, seed=91)
+    att = make_attention(batch=1, seq_len=4096, seed=92)
+    att = dataclasses.replace(att, out_proj=_proj(x.shape[1], 24 * 256, 93))
+    res = mk.decode_layer(3, x, w, full_attention=att, top_k=k)
+    ref = oracle.decode_layer(
+        np32(x), kind="full_attention", moe=_np_fields(w, MOE_FIELDS), top_k=k,
+        full_attention=dict(q=np32(att.q), k_cache=np32(att.k_cache), v_cache=np32(att.v_cache), scale=att.scale,
+                            out_proj=np32(att.out_proj)))
+    assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
+    assert_close_out(res.attention_output, ref["attention_output"])
+    assert_close_out(res.hidden, ref["hidden"])
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_decode_layer_gated_delta_with_dense_ffn(batch):
+    x, d = make_dense(batch=batch, hidden=2048, intermediate=6144, seed=100 + batch)
+    lin = make_gated_delta(batch=batch, seed=110 + batch)
+    lin = dataclasses.replace(lin, out_proj=_proj(2048, 32 * 128, 120 + batch))
+    res = mk.decode_layer(0, x, dense_ffn=d, linear_attention=lin)
+    ref = oracle.decode_layer(
+        np32(x), kind="linear_attention", dense_ffn=_np_fields(d, DENSE_FIELDS),
+        linear_attention=dict(q=np32(lin.q), k=np32(lin.k), v=np32(lin.v), state=np32(lin.state), g=np32(lin.g),
+                              beta=np32(lin.beta), out_proj=np32(lin.out_proj)))
+    assert res.router_indices is None
+    assert_close_state(res.linear_state, ref["linear_state"])
+    assert_close_out(res.hidden, ref["hidden"])
+
+
+def test_decode_layer_without_out_proj_reshapes():
+    """Without out_proj the attention output is reshaped onto the hidden size,
+    as in the reference (ops.py:722,728): 8 q heads x 256 = 2048 = hidden."""
+    x, w, k = make_moe(batch=1, seed=131)
+    att = make_attention(batch=1, q_heads=8, kv_heads=2, seq_len=300, seed=132)
+    res = mk.decode_layer(3, x, w, full_attention=att, top_k=k)
+    ref = oracle.decode_layer(
+        np32(x), kind="full_attention", moe=_np_fields(w, MOE_FIELDS), top_k=k,
+        full_attention=dict(q=np32(att.q), k_cache=np32(att.k_cache), v_cache=np32(att.v_cache), scale=att.scale))
+    assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
+    np.testing.assert_array_equal(res.attention_output.shape, x.shape)
+    assert_close_out(res.hidden, ref["hidden"])
