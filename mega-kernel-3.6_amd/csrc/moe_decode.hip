@@ -51,7 +51,7 @@ constexpr int kMaxIC = 2;      // max 16-byte chunks per lane for an intermediat
 constexpr int kGU = 2;         // routed gate/up row pairs per wave and load group (one-row path)
 constexpr int kGUM = 1;        // the same for the multi-row path, whose per-row state needs the registers
 constexpr int kDN = 8;         // down rows issued per wave before the act hand-off
-constexpr int kDS = 6;         // down rows per streamed group in the multi-row down phase
+constexpr int kRB = 8;         // output rows per block in the multi-row down phase (kRB * kMaxB == 64 lanes)
 constexpr int kMaxEL = 16;     // router logits per lane (E <= 1024)
 constexpr unsigned kSpinLimit = 1u << 21;
 
@@ -383,8 +383,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // output row are independent of the routing.  The multi-row path fetches
   // the gate/up rows now; the one-row path only once its router logits are
   // out, so that the router rows do not queue behind 6 MB of shared-expert
-  // rows.  Both fetch the down row at the end of the gate/up phase (held from
-  // here it would stay live through every phase).
+  // rows, and fetches its shared down row with them.  The multi-row path
+  // fetches its down row at the end of the gate/up phase (held from here it
+  // would stay live through every phase of that register-heavy instance).
   u32x4 sgr[HC], sur[HC], sdn[IC];
   auto issue_shared_gu = [&]() {
     load_row<T, VEC, HC>(a.sg + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sgr);
@@ -538,20 +539,40 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   const unsigned tag = gen + 1u;
   if (tid == 0) put_tagged(w.presence + wg, 0.f, tag);
 
-  // Router logits of this wave's rows.
-  for (int e = e0, r = 0; e < E; e += nwg * kWaves, ++r) {
-    if (r > 0) load_row<T, VEC, HC>(a.router + size_t(e) * H, H, true, lane, rrow);
+  // Router logits of this wave's rows.  The one-row instance owns at most one
+  // router row and one shared row per wave (the host checks E and Is against
+  // the wave count), so its code has no loads here: loads in a branch that
+  // most waves skip make the compiler wait at the join for the loads issued
+  // before it.
+  if constexpr (MB == 1) {
+    if (e0 < E) {
+      const float s = wave_sum_u(dot_row<T, HC>(rrow, xn, H, lane));
+      if (lane == 0) put_tagged(w.logits + e0, s, tag);
+    }
+  } else {
+    for (int e = e0, r = 0; e < E; e += nwg * kWaves, ++r) {
+      if (r > 0) load_row<T, VEC, HC>(a.router + size_t(e) * H, H, true, lane, rrow);
 #pragma unroll
-    for (int b = 0; b < MB; ++b)
-      if (b < B) {
-        const float s = wave_sum_u(dot_row<T, HC>(rrow, xn + b * Hp, H, lane));
-        if (lane == 0) put_tagged(w.logits + size_t(b) * E + e, s, tag);
-      }
+      for (int b = 0; b < MB; ++b)
+        if (b < B) {
+          const float s = wave_sum_u(dot_row<T, HC>(rrow, xn + b * Hp, H, lane));
+          if (lane == 0) put_tagged(w.logits + size_t(b) * E + e, s, tag);
+        }
+    }
   }
   // Shared-expert gate/up of this wave's rows.  The one-row path runs this
   // after issuing its routed loads: the shared rows arrive behind the router
   // row, and the routing must not wait for them.
   auto publish_shared = [&]() {
+    if constexpr (MB == 1) {
+      if (s0 < Is) {
+        float g = dot_row<T, HC>(sgr, xn, H, lane);
+        float u = dot_row<T, HC>(sur, xn, H, lane);
+        wave_sum2_u(g, u);
+        if (lane == 0) put_tagged(w.sact + s0, silu(g) * u, tag);
+      }
+      return;
+    }
     for (int s = s0, r = 0; s < Is; s += nwg * kWaves, ++r) {
       if (r > 0) {
         load_row<T, VEC, HC>(a.sg + size_t(s) * H, H, true, lane, sgr);
@@ -570,6 +591,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
 
   if constexpr (MB == 1) {
     issue_shared_gu();
+    issue_shared_down();  // 1 KB per wave, used in phase 3: fetched while HBM idles during the routing
     pin_loads();
     // ---- phases 1-2, one batch row ---------------------------------------------
     // Wave 0 gathers all logits and routes; the other waves wait at the
@@ -632,6 +654,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     u32x4 gA[kGU][HC], uA[kGU][HC], gB[kGU][HC], uB[kGU][HC];
     issue_gu(gw, gA, uA);
     pin_loads();
+    // Shared-expert act of the waves that own a shared row (its rows arrived
+    // long ago), before their routed rows: phase 3 needs both.  This code
+    // issues no loads (one shared row per wave), so it adds no wait for the
+    // gate/up rows just issued.
     publish_shared();
     for (int t0 = gw; t0 < ntask; t0 += 2 * step) {
       if (t0 + step < ntask) issue_gu(t0 + step, gB, uB);
@@ -651,7 +677,6 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     for (int s = 0; s < kDN; ++s)
       load_row<T, VEC, IC>(a.ed + (size_t(slot_expert(min(s, K - 1))) * H + hrow) * I, I, s < K && wave < nrows, lane,
                            dn[s]);
-    issue_shared_down();
     pin_loads();
 
     // ---- phase 3, one batch row ----------------------------------------------
@@ -894,14 +919,14 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     pin_loads();
     compute_gu(t0 + step, gB, uB);
   }
-  // Down rows of (output row h0 + wave, expert u = j), issued only now: they
-  // stream while act is handed over instead of competing with the gate/up
-  // rows on which act depends.
-  u32x4 dn[kDN][IC];
+  // Down rows of this wave's first expert (u = wave) for the WG's first block
+  // of output rows, issued only now: they stream while act is handed over
+  // instead of competing with the gate/up rows on which act depends.
+  u32x4 dn[kRB][IC];
 #pragma unroll
-  for (int j = 0; j < kDN; ++j)
-    load_row<T, VEC, IC>(a.ed + (size_t(ulist[min(j, U - 1)]) * H + min(h0 + wave, H - 1)) * I, I,
-                         j < U && wave < nrows, lane, dn[j]);
+  for (int r = 0; r < kRB; ++r)
+    load_row<T, VEC, IC>(a.ed + (size_t(ulist[min(wave, U - 1)]) * H + min(h0 + r, H - 1)) * I, I,
+                         wave < U && r < nrows, lane, dn[r]);
   issue_shared_down();
   pin_loads();
   __syncthreads();  // x_norm (region A) is dead from here on
@@ -936,113 +961,133 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       sact_l[t] = val;
     }
   }
-  // Wave w owns output rows hl = w, w + kWaves, ...: it sums its experts in
-  // ascending expert order (wave-uniform values), keeping the running sums in
-  // part[hl][b] between act windows, then adds the gated shared expert and
-  // the residual and writes the row.  The down rows of (hl = w, expert u < kDN)
-  // were issued in phase 2.
+  // Down projection by experts: wave w takes experts u_lo + w, u_lo + w + 8,
+  // ... of each act window and, for each, the down rows of the WG's block of
+  // kRB output rows -- kRB contiguous rows (kRB KB at I = 512), read as whole
+  // cache lines.  Every lane keeps partials acc[r][b] for all rows and batch
+  // rows over all windows; one butterfly reduction across the lanes at the end
+  // leaves lane L with the total of accumulator bitrev(L), and the waves'
+  // totals meet in LDS.  Usually nrows <= kRB (one block).
   for (int t = tid; t < a.rows_per_wg * MB; t += kThreads) part[t] = 0.f;
-  // Windows of whole experts, at most win_entries act rows each (the host
-  // sizes the window for at least kMaxB rows, one expert's worst case).
   const int win_entries = a.win_floats / Ip;
-  int u_lo = 0;
-  while (u_lo < U) {
-    int u_hi = u_lo + 1;
-    while (u_hi < U && ent_base[u_hi + 1] - ent_base[u_lo] <= win_entries) ++u_hi;
-    const int e_lo = ent_base[u_lo], ent = ent_base[u_hi] - e_lo;
-    __syncthreads();  // previous window fully consumed
-    if constexpr (VEC) {
-      const rsrc_t ar = make_rsrc(w.act, uint32_t(B) * uint32_t(K) * uint32_t(I) * 8u);
-      const int hp = Ip / 2;
-      ok3 = gather_tagged_pairs(
-                ar, ent * hp,
-                [&](int f) -> uint32_t {
-                  const int en = f / hp, c2 = (f % hp) * 2;
-                  return c2 < I ? uint32_t(ent_src[e_lo + en] * I + c2) * 8u : 0xFFFFFFF0u;
-                },
-                act_l, tag, tid) &&
-            ok3;
-    } else {
-      for (int t = tid; t < ent * Ip; t += kThreads) {
-        const int en = t / Ip, i = t % Ip;
-        float val = 0.f;
-        if (i < I) {
-          uint64_t word = 0;
-          const uint64_t* pw = w.act + size_t(ent_src[e_lo + en]) * I + i;
-          for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
-            word = __hip_atomic_load(const_cast<uint64_t*>(pw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (unsigned(word >> 32) == tag) break;
-            __builtin_amdgcn_s_sleep(1);
+  for (int rb = 0; rb < nrows; rb += kRB) {
+    const int nr = min(kRB, nrows - rb);
+    float acc[kRB][MB];
+#pragma unroll
+    for (int r = 0; r < kRB; ++r)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) acc[r][b] = 0.f;
+    int u_lo = 0;
+    while (u_lo < U) {
+      int u_hi = u_lo + 1;
+      while (u_hi < U && ent_base[u_hi + 1] - ent_base[u_lo] <= win_entries) ++u_hi;
+      const int e_lo = ent_base[u_lo], ent = ent_base[u_hi] - e_lo;
+      __syncthreads();  // previous window (and part[] zeroing) done
+      if constexpr (VEC) {
+        const rsrc_t ar = make_rsrc(w.act, uint32_t(B) * uint32_t(K) * uint32_t(I) * 8u);
+        const int hp = Ip / 2;
+        ok3 = gather_tagged_pairs(
+                  ar, ent * hp,
+                  [&](int f) -> uint32_t {
+                    const int en = f / hp, c2 = (f % hp) * 2;
+                    return c2 < I ? uint32_t(ent_src[e_lo + en] * I + c2) * 8u : 0xFFFFFFF0u;
+                  },
+                  act_l, tag, tid) &&
+              ok3;
+      } else {
+        for (int t = tid; t < ent * Ip; t += kThreads) {
+          const int en = t / Ip, i = t % Ip;
+          float val = 0.f;
+          if (i < I) {
+            uint64_t word = 0;
+            const uint64_t* pw = w.act + size_t(ent_src[e_lo + en]) * I + i;
+            for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
+              word = __hip_atomic_load(const_cast<uint64_t*>(pw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              if (unsigned(word >> 32) == tag) break;
+              __builtin_amdgcn_s_sleep(1);
+            }
+            ok3 = ok3 && unsigned(word >> 32) == tag;
+            val = __uint_as_float(unsigned(word));
           }
-          ok3 = ok3 && unsigned(word >> 32) == tag;
-          val = __uint_as_float(unsigned(word));
+          act_l[t] = val;
         }
-        act_l[t] = val;
       }
-    }
-    if (!ok3) misc[16] = 1;
-    __syncthreads();
-    for (int hl = wave; hl < nrows; hl += kWaves) {
-      // Lane partials over this window's experts; one wave reduction per
-      // batch row at the end of the window.
-      float accl[MB];
+      if (!ok3) misc[16] = 1;
+      __syncthreads();
+      // Rows of expert u for the block (zero-size loads past the window or
+      // past the block), issued unconditionally so that the waits before a
+      // block's use cover only that block.
+      auto issue_x = [&](int u, u32x4 (&c)[kRB][IC]) {
+        const size_t base = (size_t(ulist[min(u, U - 1)]) * H + h0 + rb) * I;
 #pragma unroll
-      for (int b = 0; b < MB; ++b) accl[b] = 0.f;
-      auto add_expert = [&](int u, const u32x4 (&c)[IC]) {
-        if constexpr (MB == 1) {  // one row: expert u's act is window entry u - u_lo
-          accl[0] += dot_row<T, IC>(c, act_l + size_t(u - u_lo) * Ip, I, lane);
-        } else {
-          const unsigned mask = umask[u];
-#pragma unroll
-          for (int b = 0; b < MB; ++b)
-            if ((mask >> b) & 1u)
-              accl[b] += dot_row<T, IC>(c, act_l + size_t(ent_of[u * MB + b] - e_lo) * Ip, I, lane);
-        }
+        for (int r = 0; r < kRB; ++r)
+          load_row<T, VEC, IC>(a.ed + base + size_t(min(r, nr - 1)) * I, I, u < u_hi && r < nr, lane, c[r]);
       };
-      int u_next = u_lo;
-      if (hl == wave) {  // prefetched rows first (experts u < kDN, ascending)
+      auto consume_x = [&](int u, const u32x4 (&c)[kRB][IC]) {
+        if (u >= u_hi) return;
+        const unsigned mask = umask[u];
 #pragma unroll
-        for (int uu = 0; uu < kDN; ++uu)
-          if (uu >= u_lo && uu < u_hi) add_expert(uu, dn[uu]);
-        u_next = max(u_lo, kDN);
+        for (int b = 0; b < MB; ++b)
+          if ((mask >> b) & 1u) {
+            const float* av = act_l + size_t(ent_of[u * MB + b] - e_lo) * Ip;
+#pragma unroll
+            for (int r = 0; r < kRB; ++r) acc[r][b] += dot_row<T, IC>(c[r], av, I, lane);
+          }
+      };
+      u32x4 ca[kRB][IC], cb[kRB][IC];
+      int u = u_lo + wave;
+      if (rb == 0 && u_lo == 0 && wave < u_hi) {  // prefetched in phase 2
+#pragma unroll
+        for (int r = 0; r < kRB; ++r)
+#pragma unroll
+          for (int q = 0; q < IC; ++q) ca[r][q] = dn[r][q];
+      } else {
+        issue_x(u, ca);
       }
-      // The remaining down rows stream in groups of kDS, two groups in flight:
-      // the next group is issued before the current one is consumed.  Groups
-      // are issued unconditionally (rows past u_hi are zero-size loads), so
-      // the waits before a group's use cover only that group.
-      const size_t rowoff = size_t(h0 + hl) * I;
-      auto issue_ds = [&](int ub, u32x4 (&c)[kDS][IC]) {
-#pragma unroll
-        for (int j = 0; j < kDS; ++j) {
-          const int u = ub + j;
-          load_row<T, VEC, IC>(a.ed + size_t(ulist[min(u, U - 1)]) * H * I + rowoff, I, u < u_hi, lane, c[j]);
-        }
-      };
-      auto consume_ds = [&](int ub, const u32x4 (&c)[kDS][IC]) {
-#pragma unroll
-        for (int j = 0; j < kDS; ++j)
-          if (ub + j < u_hi) add_expert(ub + j, c[j]);
-      };
-      if (u_next < u_hi) {
-        u32x4 da[kDS][IC], db[kDS][IC];
-        issue_ds(u_next, da);
+      pin_loads();
+      for (; u < u_hi; u += 2 * kWaves) {
+        issue_x(u + kWaves, cb);
         pin_loads();
-        for (int ub = u_next; ub < u_hi; ub += 2 * kDS) {
-          issue_ds(ub + kDS, db);
-          pin_loads();
-          consume_ds(ub, da);
-          issue_ds(ub + 2 * kDS, da);
-          pin_loads();
-          consume_ds(ub + kDS, db);
-        }
+        consume_x(u, ca);
+        issue_x(u + 2 * kWaves, ca);
+        pin_loads();
+        consume_x(u + kWaves, cb);
       }
+      u_lo = u_hi;
+    }
+    // Butterfly: at step k the lane keeps the half of its accumulators picked
+    // by lane bit k and adds the partner's (lane ^ 2^k) copy of that half.
+    constexpr int NA = kRB * MB;  // == kWave
+    static_assert(NA == kWave, "one accumulator per lane after the butterfly");
+    float v[NA];
 #pragma unroll
-      for (int b = 0; b < MB; ++b) {
-        const float t = wave_sum_u(accl[b]);
-        if (lane == 0) part[hl * MB + b] += t;
+    for (int r = 0; r < kRB; ++r)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) v[r * MB + b] = acc[r][b];
+#pragma unroll
+    for (int k = 0; (1 << k) < NA; ++k) {
+      const int half = NA >> (k + 1);
+      const bool hi = (lane >> k) & 1;
+#pragma unroll
+      for (int i = 0; i < half; ++i) {
+        const float keep = hi ? v[i + half] : v[i];
+        const float send = hi ? v[i] : v[i + half];
+        v[i] = keep + __shfl_xor(send, 1 << k, kWave);
       }
     }
-    u_lo = u_hi;
+    int idx = 0;  // bit-reversed lane: the accumulator this lane now holds
+#pragma unroll
+    for (int k = 0; (1 << k) < NA; ++k) idx |= ((lane >> k) & 1) << (5 - k);
+    __syncthreads();  // act window dead: its first kWaves * NA floats take the wave totals
+    act_l[wave * NA + idx] = v[0];
+    __syncthreads();
+    if (tid < NA) {
+      const int r = tid / MB, b = tid % MB;
+      float t = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) t += act_l[ww * NA + tid];
+      if (r < nr) part[(rb + r) * MB + b] = t;
+    }
   }
   __syncthreads();
   timed_out = misc[16] != 0;
@@ -1120,19 +1165,23 @@ int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
   const size_t avail = limit > fixed ? limit - fixed : 0;
   const size_t want = size_t(kMaxB) * a.K * Ip;
   const size_t room = avail > size_t(kMaxB) * Isp ? avail - size_t(kMaxB) * Isp : 0;
-  const size_t win = (room < want ? room : want) / Ip * Ip;
-  if (avail < size_t(kMaxB) * Hp || win < size_t(kMaxB) * Ip)
-    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: shape does not fit the %zu bytes of LDS", limit * 4);
-  a.win_floats = int(win);
+  // The window area also takes the multi-row down phase's per-wave totals
+  // (kWaves * kWave floats) once the last window is consumed.
+  const size_t totals = (size_t(kWaves) * kWave + Ip - 1) / Ip * Ip;
+  const size_t win = max(totals, (room < want ? room : want) / Ip * Ip);
   const size_t region_floats = max(size_t(kMaxB) * Hp, win + size_t(kMaxB) * Isp);
   const size_t lds = 4 * (fixed + region_floats);
+  if (avail < size_t(kMaxB) * Hp || win < size_t(kMaxB) * Ip || fixed + region_floats > limit)
+    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: shape does not fit the %zu bytes of LDS", limit * 4);
+  a.win_floats = int(win);
   // Chunk counts per lane: the smallest instantiation that covers the rows.
   const int hc_need = (a.H + EPC * kWave - 1) / (EPC * kWave);
   const int ic_need = (max(a.I, a.Is) + EPC * kWave - 1) / (EPC * kWave);
   // The one-row path keeps x_norm, act [K][Ip] and the shared act side by side
   // in the LDS region that the multi-row path shares between them.
   const size_t one_row_floats = Hp + size_t(a.K) * Ip + Isp;
-  const bool one_row_ok = batch == 1 && one_row_floats <= max(Hp, win + Isp);  // region A as sized for B = 1
+  const bool one_row_ok = batch == 1 && one_row_floats <= max(Hp, win + Isp) &&  // region A as sized for B = 1
+                          a.E <= nwg * kWaves && a.Is <= nwg * kWaves;           // one router / shared row per wave
   const int which = (vec && hc_need <= 4 && ic_need <= 1) ? (one_row_ok ? 0 : 1) : (vec ? 2 : 3);
   const bool el4 = a.E <= 4 * kWave;
   void (*kern)(MoeArgs<T>) = which == 0   ? (el4 ? &moe_decode_kernel<T, true, 4, 1, 1, 4>
