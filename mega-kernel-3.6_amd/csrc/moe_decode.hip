@@ -355,14 +355,26 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   u32x4 xc[4], nc[4], gc[4];
   const rsrc_t gsr = make_rsrc(a.wsg, a.wsg != nullptr ? uint32_t(H) * uint32_t(sizeof(T)) : 0u);
   if constexpr (VEC) {
-    const rsrc_t xr = make_rsrc(a.x, uint32_t(B) * uint32_t(H) * uint32_t(sizeof(T)));
     const rsrc_t nr = make_rsrc(a.nw, uint32_t(H) * uint32_t(sizeof(T)));
+    if constexpr (MB == 1) {
+      const rsrc_t xr = make_rsrc(a.x, uint32_t(B) * uint32_t(H) * uint32_t(sizeof(T)));
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int q = tid + r * kThreads;
-      xc[r] = buf_load16(xr, q < B * hq ? uint32_t(q) * 16u : 0xFFFFFFF0u);
-      nc[r] = buf_load16(nr, uint32_t(q % hq) * 16u);
-      gc[r] = buf_load16(gsr, uint32_t(q % hq) * 16u);
+      for (int r = 0; r < 4; ++r) {
+        const int q = tid + r * kThreads;
+        xc[r] = buf_load16(xr, q < B * hq ? uint32_t(q) * 16u : 0xFFFFFFF0u);
+        nc[r] = buf_load16(nr, uint32_t(q % hq) * 16u);
+        gc[r] = buf_load16(gsr, uint32_t(q % hq) * 16u);
+      }
+    } else {
+      // Several rows: wave b normalises batch row b (chunk lane + 64 r).
+      const rsrc_t xr = make_rsrc(a.x + size_t(min(wave, B - 1)) * H, wave < B ? uint32_t(H) * uint32_t(sizeof(T)) : 0u);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t off = uint32_t(lane + kWave * r) * 16u;
+        xc[r] = buf_load16(xr, off);
+        nc[r] = buf_load16(nr, off);
+        gc[r] = buf_load16(gsr, off);
+      }
     }
   }
   // Generation of this launch (advanced by WG 0 at the end of the previous
@@ -373,10 +385,15 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // the expert weights have streamed through, x is no longer in the L2.
   float x_res = 0.f;
   if constexpr (MB == 1) x_res = to_f(a.x[min(wg * a.rows_per_wg + wave, H - 1)]);
-  const int e0 = wg + nwg * wave;  // first router row of this wave
+  // Router and shared gate/up rows: one row per wave (rows wg + nwg * w) with
+  // one batch row; with several batch rows, wave b takes every router and
+  // shared row of the WG (rows wg + nwg * j) for batch row b.
+  const int e0 = MB == 1 ? wg + nwg * wave : wg;  // first router row of this wave
+  const int rstep = MB == 1 ? nwg * kWaves : nwg;
+  const bool rows_on = MB == 1 || wave < B;
   u32x4 rrow[HC];
-  load_row<T, VEC, HC>(a.router + size_t(min(e0, E - 1)) * H, H, e0 < E, lane, rrow);
-  const int s0 = wg + nwg * (kWaves - 1 - wave);  // first shared gate/up row of this wave
+  load_row<T, VEC, HC>(a.router + size_t(min(e0, E - 1)) * H, H, e0 < E && rows_on, lane, rrow);
+  const int s0 = MB == 1 ? wg + nwg * (kWaves - 1 - wave) : wg;  // first shared gate/up row of this wave
   const int h0 = wg * a.rows_per_wg;
   const int nrows = max(0, min(a.rows_per_wg, H - h0));
   // Shared-expert gate/up rows and the shared down row of this wave's first
@@ -388,8 +405,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // would stay live through every phase of that register-heavy instance).
   u32x4 sgr[HC], sur[HC], sdn[IC];
   auto issue_shared_gu = [&]() {
-    load_row<T, VEC, HC>(a.sg + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sgr);
-    load_row<T, VEC, HC>(a.su + size_t(min(s0, Is - 1)) * H, H, s0 < Is, lane, sur);
+    load_row<T, VEC, HC>(a.sg + size_t(min(s0, Is - 1)) * H, H, s0 < Is && rows_on, lane, sgr);
+    load_row<T, VEC, HC>(a.su + size_t(min(s0, Is - 1)) * H, H, s0 < Is && rows_on, lane, sur);
   };
   auto issue_shared_down = [&]() {
     load_row<T, VEC, IC>(a.sd + size_t(min(h0 + wave, H - 1)) * Is, Is, wave < nrows, lane, sdn);
@@ -397,9 +414,83 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   if constexpr (MB > 1) issue_shared_gu();
   pin_loads();
 
-  if constexpr (MB > 1)
+  if constexpr (MB > 1) {
     for (int e = tid; e < E; e += kThreads) emask[e] = 0u;
-  {
+    // Wave b: RMSNorm of batch row b into LDS and its shared-gate dot; no
+    // other wave reads the row before the routing barrier.
+    if (tid == 0) misc[16] = 0;
+    if (wave < B) {
+      float* xr_l = xn + wave * Hp;
+      float ss = 0.f;
+      auto sq_chunk = [&](int c, const u32x4& xq, const u32x4& nq) {
+        float xf[EPC], nf[EPC];
+        unpack(xq, xf, T{});
+        unpack(nq, nf, T{});
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) ss = fmaf(xf[e], xf[e], ss);
+        if (c < hq) {
+          float4* dst = reinterpret_cast<float4*>(xr_l + c * EPC);
+#pragma unroll
+          for (int h = 0; h < EPC / 4; ++h)
+            dst[h] = make_float4(xf[4 * h] * nf[4 * h], xf[4 * h + 1] * nf[4 * h + 1], xf[4 * h + 2] * nf[4 * h + 2],
+                                 xf[4 * h + 3] * nf[4 * h + 3]);
+        }
+      };
+      if constexpr (VEC) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sq_chunk(lane + kWave * r, xc[r], nc[r]);
+        if constexpr (HC > 4) {
+          const rsrc_t xr = make_rsrc(a.x + size_t(wave) * H, uint32_t(H) * uint32_t(sizeof(T)));
+          const rsrc_t nr = make_rsrc(a.nw, uint32_t(H) * uint32_t(sizeof(T)));
+          for (int c = lane + 4 * kWave; c < hq; c += kWave)
+            sq_chunk(c, buf_load16(xr, uint32_t(c) * 16u), buf_load16(nr, uint32_t(c) * 16u));
+        }
+      } else {
+        for (int h = lane; h < Hp; h += kWave) {
+          const float v = h < H ? to_f(a.x[size_t(wave) * H + h]) : 0.f;
+          const float nwv = h < H ? to_f(a.nw[h]) : 0.f;
+          ss = fmaf(v, v, ss);
+          xr_l[h] = v * nwv;
+        }
+      }
+      const float inv = 1.0f / sqrtf(wave_sum_u(ss) / float(H) + a.eps);
+      float dg = 0.f;
+      if constexpr (VEC) {
+        auto scale_chunk = [&](int c, const u32x4& gq) {
+          if (c >= hq) return;
+          float gf[EPC];
+          unpack(gq, gf, T{});
+          float4* xv = reinterpret_cast<float4*>(xr_l + c * EPC);
+#pragma unroll
+          for (int h = 0; h < EPC / 4; ++h) {
+            float4 v = xv[h];
+            v.x *= inv;
+            v.y *= inv;
+            v.z *= inv;
+            v.w *= inv;
+            xv[h] = v;
+            dg = fmaf(v.x, gf[4 * h], dg);
+            dg = fmaf(v.y, gf[4 * h + 1], dg);
+            dg = fmaf(v.z, gf[4 * h + 2], dg);
+            dg = fmaf(v.w, gf[4 * h + 3], dg);
+          }
+        };
+#pragma unroll
+        for (int r = 0; r < 4; ++r) scale_chunk(lane + kWave * r, gc[r]);
+        if constexpr (HC > 4)
+          for (int c = lane + 4 * kWave; c < hq; c += kWave) scale_chunk(c, buf_load16(gsr, uint32_t(c) * 16u));
+      } else {
+        for (int h = lane; h < Hp; h += kWave) {
+          const float v = xr_l[h] * inv;
+          xr_l[h] = v;
+          dg = fmaf(v, (a.wsg != nullptr && h < H) ? to_f(a.wsg[h]) : 0.f, dg);
+        }
+      }
+      const float t = wave_sum_u(dg);
+      if (lane == 0) sgf[wave] = a.wsg != nullptr ? 1.0f / (1.0f + expf(-t)) : 1.0f;
+    }
+    __syncthreads();  // emask and misc cleared before phase 1
+  } else   {
     float ss[MB], gs[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b) ss[b] = gs[b] = 0.f;
@@ -549,15 +640,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       const float s = wave_sum_u(dot_row<T, HC>(rrow, xn, H, lane));
       if (lane == 0) put_tagged(w.logits + e0, s, tag);
     }
-  } else {
-    for (int e = e0, r = 0; e < E; e += nwg * kWaves, ++r) {
+  } else if (wave < B) {
+    for (int e = e0, r = 0; e < E; e += rstep, ++r) {
       if (r > 0) load_row<T, VEC, HC>(a.router + size_t(e) * H, H, true, lane, rrow);
-#pragma unroll
-      for (int b = 0; b < MB; ++b)
-        if (b < B) {
-          const float s = wave_sum_u(dot_row<T, HC>(rrow, xn + b * Hp, H, lane));
-          if (lane == 0) put_tagged(w.logits + size_t(b) * E + e, s, tag);
-        }
+      const float s = wave_sum_u(dot_row<T, HC>(rrow, xn + wave * Hp, H, lane));
+      if (lane == 0) put_tagged(w.logits + size_t(wave) * E + e, s, tag);
     }
   }
   // Shared-expert gate/up of this wave's rows.  The one-row path runs this
@@ -573,18 +660,16 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       }
       return;
     }
-    for (int s = s0, r = 0; s < Is; s += nwg * kWaves, ++r) {
+    if (wave >= B) return;
+    for (int s = s0, r = 0; s < Is; s += rstep, ++r) {
       if (r > 0) {
         load_row<T, VEC, HC>(a.sg + size_t(s) * H, H, true, lane, sgr);
         load_row<T, VEC, HC>(a.su + size_t(s) * H, H, true, lane, sur);
       }
-#pragma unroll
-      for (int b = 0; b < MB; ++b)
-        if (b < B) {
-          const float g = wave_sum_u(dot_row<T, HC>(sgr, xn + b * Hp, H, lane));
-          const float u = wave_sum_u(dot_row<T, HC>(sur, xn + b * Hp, H, lane));
-          if (lane == 0) put_tagged(w.sact + size_t(b) * Is + s, silu(g) * u, tag);
-        }
+      float g = dot_row<T, HC>(sgr, xn + wave * Hp, H, lane);
+      float u = dot_row<T, HC>(sur, xn + wave * Hp, H, lane);
+      wave_sum2_u(g, u);
+      if (lane == 0) put_tagged(w.sact + size_t(wave) * Is + s, silu(g) * u, tag);
     }
   };
   if constexpr (MB > 1) publish_shared();
