@@ -284,11 +284,25 @@ def bench_layer(mk, inputs, timer, steps, warmup, batches):
                   + moe_bytes(b, 2048, 256, 512, 512, k, distinct))
         fn = lambda: mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)  # noqa: E731
         cold = measure(timer, fn, steps, warmup, nbytes)
+        # The same layer replayed from a HIP graph (captured on a stream whose
+        # workspaces already exist): no per-op launch gaps.
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        cold["graph_median_us"] = timer.pipelined(graph.replay, steps, cold=True)
         out[f"layer_linear_moe_b{b}"] = cold
         log(f"decode_layer (gated delta + out_proj + MoE) b={b}: {cold['median_us']:.2f} us cold in stream "
             f"({cold['gbps']:.0f} GB/s), {cold['warm_median_us']:.2f} us warm, "
-            f"{cold['isolated_event_median_us']:.2f} us isolated launch")
-        del x, w, lin
+            f"{cold['isolated_event_median_us']:.2f} us isolated launch, {cold['graph_median_us']:.2f} us graph replay")
+        del x, w, lin, graph
         torch.cuda.empty_cache()
     return out
 

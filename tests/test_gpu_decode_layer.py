@@ -98,3 +98,32 @@ def test_decode_layer_without_out_proj_reshapes():
     assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
     np.testing.assert_array_equal(res.attention_output.shape, x.shape)
     assert_close_out(res.hidden, ref["hidden"])
+
+
+def test_decode_layer_graph_replay():
+    """A captured decode_layer (gated delta + out_proj + MoE) replays bit-identically
+    to eager calls.  The capture stream's workspaces exist before capture, so the
+    graph holds no workspace fill: every replay relies on the MoE generation word
+    and the arrival counters left by the previous call."""
+    x, w, k = make_moe(batch=1, seed=141)
+    lin = make_gated_delta(batch=1, seed=142)
+    lin = dataclasses.replace(lin, out_proj=_proj(x.shape[1], 32 * 128, 143))
+    eager = mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        res = mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(res.hidden, eager.hidden)
+        assert torch.equal(res.router_indices, eager.router_indices)
+        assert torch.equal(res.linear_state, eager.linear_state)
+        mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)  # eager work between replays
+        torch.cuda.synchronize()
