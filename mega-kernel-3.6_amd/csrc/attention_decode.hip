@@ -47,6 +47,7 @@ constexpr int kMaxChunks = 1024;
 constexpr int kMergeThreads = 1024;
 constexpr int kMergeSlices = kMergeThreads / kWave;
 constexpr int kMergeBatch = 8;           // chunk loads in flight per merge thread
+static_assert(kMaxChunks <= kMergeThreads, "the merge kernel holds one chunk's (m, l) per thread");
 constexpr uint32_t kFar = 0x80000000u;   // pushes an offset past any descriptor (all < 2^31 bytes)
 constexpr float kNegInf = -INFINITY;
 
@@ -306,24 +307,22 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* 
   for (int k = 0; k < kMergeBatch; ++k) pv[k] = buf_loadf(por, uint32_t(sl + kMergeSlices * k) * d * 4 + doff);
   pin_loads();
 
-  const float* pm = part_m + size_t(bq) * nch;
-  const float* pl = part_l + size_t(bq) * nch;
-  float M = kNegInf;
-  for (int c = tid; c < nch; c += kMergeThreads) M = fmaxf(M, pm[c]);
-  M = wave_max(M);
+  // Thread c holds chunk c's (m, l) (nch <= kMaxChunks <= kMergeThreads); both
+  // are loaded with the partial-O batch, so one memory latency covers all.
+  const rsrc_t pmr = make_rsrc(part_m + size_t(bq) * nch, uint32_t(nch) * 4);
+  const rsrc_t plr = make_rsrc(part_l + size_t(bq) * nch, uint32_t(nch) * 4);
+  const float m_ld = buf_loadf(pmr, uint32_t(tid) * 4);
+  const float lc = buf_loadf(plr, uint32_t(tid) * 4);
+  const float mc = tid < nch ? m_ld : kNegInf;
+  float M = wave_max(mc);
   if (dl == 0) rw[0][sl] = M;
   __syncthreads();
   M = rw[0][0];
 #pragma unroll
   for (int s = 1; s < kMergeSlices; ++s) M = fmaxf(M, rw[0][s]);
-  float L = 0.f;
-  for (int c = tid; c < nch; c += kMergeThreads) {
-    const float mc = pm[c];
-    const float w = mc == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mc - M);
-    wgt[c] = w;
-    L += w * pl[c];
-  }
-  L = wave_sum(L);
+  const float w = mc == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mc - M);
+  if (tid < nch) wgt[tid] = w;
+  float L = wave_sum(w * lc);
   if (dl == 0) rw[1][sl] = L;
   __syncthreads();
   L = 0.f;
@@ -403,9 +402,13 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(const T* __restr
   }
 }
 
-// Chunk geometry: about two workgroups per CU over all units, at least one
-// tile per wave, and every chunk's byte range addressable with 31-bit offsets
-// (including the prefetch one pass past its end).
+// Chunk geometry: enough workgroups per CU for about 64 KB of K/V in flight
+// (each wave holds one 16-token K+V tile: one workgroup per CU at D = 256,
+// two at 128, four at 64), at least one tile per wave, and every chunk's byte
+// range addressable with 31-bit offsets (including the prefetch one pass past
+// its end).  More bytes in flight than that only lengthens the HBM queue: with
+// two workgroups per CU at D = 256 each tile takes ~4.5 us instead of ~2.2 us
+// to arrive, and the waves' finishing times spread over ~12 us instead of ~5.
 struct Chunking {
   int nch;
   int chunk_tokens;
@@ -416,8 +419,14 @@ int max_chunks(int seq) {
   return m < kMaxChunks ? m : kMaxChunks;
 }
 
+int wgs_per_cu(int d, size_t elt) {
+  const int tile_bytes = 2 * kTT * d * int(elt);  // one wave's K+V tile
+  const int fit = (64 << 10) / (kWaves * tile_bytes);
+  return fit > 1 ? fit : 1;
+}
+
 int plan_chunks(int units, int hkv, int d, int seq, size_t elt, Chunking* out) {
-  int nch = (2 * cu_count() + units - 1) / units;
+  int nch = (wgs_per_cu(d, elt) * cu_count() + units - 1) / units;
   const int cap = (seq + kWgTokens - 1) / kWgTokens;
   nch = nch < cap ? nch : cap;
   nch = nch < 1 ? 1 : nch;
