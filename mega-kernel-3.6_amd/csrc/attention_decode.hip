@@ -98,7 +98,7 @@ __host__ __device__ inline size_t merge_floats(int d, int heads) { return size_t
 template <int DT>
 size_t chunk_lds_bytes(int d, int heads) {
   const size_t stage = size_t(kWaves) * stage_bytes(DT);
-  const size_t merge = size_t(kWaves) * merge_floats(d, heads) * 4;
+  const size_t merge = (size_t(kWaves) * merge_floats(d, heads) + 16 * 8) * 4;  // + per-head weights
   return stage > merge ? stage : merge;
 }
 
@@ -171,8 +171,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, uint32_t(t0) * tsb + voff[i]);
   pin_loads();
 
-  const int ntiles = len > t0 ? (len - t0 + kWgTokens - 1) / kWgTokens : 0;
-  for (int it = 0; it < ntiles; ++it, t0 += kWgTokens) {
+  // One 16-token tile whose K and V are in kreg/vreg; with `pf` the next
+  // pass's tile is prefetched into them.  The last tile prefetches nothing:
+  // loads past the chunk read zero but still take a memory round trip, which
+  // the registers' reuse after the loop would wait for.
+  auto tile = [&](int t0, bool pf) __attribute__((always_inline)) {
     // Stage K, then S^T = K Q^T: sacc[i] = score(token t0 + 4grp + i, head col);
     // lane (token col, grp) reads dims 32 s + 8 grp of its token row.
 #pragma unroll
@@ -181,9 +184,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
       *reinterpret_cast<u32x4*>(stage + (qi / CPR) * KSTR + (qi % CPR) * 16) = kreg[i];
     }
     const uint32_t next = uint32_t(t0 + kWgTokens) * tsb;
+    if (pf) {
 #pragma unroll
-    for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(kr, next + voff[i]);
-    pin_loads();
+      for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(kr, next + voff[i]);
+      pin_loads();
+    }
     f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -220,9 +225,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
       dst[0] = make_uint2(vreg[i].x, vreg[i].y);
       dst[1] = make_uint2(vreg[i].z, vreg[i].w);
     }
+    if (pf) {
 #pragma unroll
-    for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, next + voff[i]);
-    pin_loads();
+      for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, next + voff[i]);
+      pin_loads();
+    }
 
     // O^T += V^T P^T: A operand = V[tokens 4grp..4grp+3][dim 16n + col] read transposed.
 #pragma unroll
@@ -235,7 +242,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
       for (int j = 0; j < 4; ++j) va.u[j] = vt[(4 * grp + j) * VSTR + 16 * n + col];
       oacc[n] = Mfma<T>::pv(va.v, pop, oacc[n] * alpha);
     }
-  }
+  };
+  const int ntiles = len > t0 ? (len - t0 + kWgTokens - 1) / kWgTokens : 0;
+  for (int it = 0; it + 1 < ntiles; ++it, t0 += kWgTokens) tile(t0, true);
+  if (ntiles > 0) tile(t0, false);
 
   // Per-head l over the 4 lane groups (m is already equal across them).
   l_run += xor_lane(l_run, 16);
@@ -258,26 +268,44 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     }
   }
   __syncthreads();
+  // Per-head weights of the 4 waves' partials (lane = head of wave 0): f_w =
+  // 2^(m_w - M), M and L = sum f_w l_w, kept in `stat` [16][8].
   const float* m0 = reinterpret_cast<const float*>(smem);
-  for (int idx = threadIdx.x; idx < heads_here * d; idx += kThreads) {
-    const int hd = idx / d, dim = idx - hd * d;
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m0[w * wstride + hd]);
-    float o = 0.f, L = 0.f;
+  float* stat = reinterpret_cast<float*>(smem) + kWaves * wstride;
+  if (wave == 0 && lane < heads_here) {
+    float mv[kWaves], M = kNegInf, L = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float mwv = m0[w * wstride + hd];
-      const float f = mwv == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mwv - M);
-      o += f * m0[w * wstride + 32 + hd * ostr + dim];
-      L += f * m0[w * wstride + 16 + hd];
+      mv[w] = m0[w * wstride + lane];
+      M = fmaxf(M, mv[w]);
     }
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = mv[w] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mv[w] - M);
+      stat[lane * 8 + w] = f;
+      L += f * m0[w * wstride + 16 + lane];
+    }
+    stat[lane * 8 + 4] = M;
+    stat[lane * 8 + 5] = L;
+  }
+  __syncthreads();
+  // Wave w merges heads w, w + 4, ...; lane l takes dims 4l..4l+3 (d <= 256).
+  const int dim = 4 * lane;
+  for (int hd = wave; hd < heads_here; hd += kWaves) {
+    if (dim >= d) continue;
+    const f32x4 fw = *reinterpret_cast<const f32x4*>(stat + hd * 8);
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      o += fw[w] * *reinterpret_cast<const f32x4*>(m0 + w * wstride + 32 + hd * ostr + dim);
+    const float M = stat[hd * 8 + 4], L = stat[hd * 8 + 5];
     const size_t bq = size_t(b) * hq + qh0 + hd;
     if (nch == 1) {
-      out[bq * d + dim] = from_f<T>(o / L);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[bq * d + dim + k] = from_f<T>(o[k] / L);
     } else {
       const size_t pi = bq * nch + c;
-      part_o[pi * d + dim] = o;
+      *reinterpret_cast<f32x4*>(part_o + pi * d + dim) = o;
       if (dim == 0) {
         part_m[pi] = M;
         part_l[pi] = L;
@@ -526,6 +554,8 @@ extern "C" int mkq_full_attention_decode(int dtype, const void* q, const void* k
   MKQ_REQUIRE(workspace && workspace_bytes >= mkq_full_attention_decode_workspace_bytes(batch, q_heads, kv_heads,
                                                                                         head_dim, seq_len),
               "full_attention_decode: workspace too small");
+  MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
+              "full_attention_decode: workspace must be 256-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* ws = static_cast<float*>(workspace);
   const bool fast_ok = (head_dim % 8 == 0) && aligned16(q) && aligned16(k_cache) && aligned16(v_cache);

@@ -164,6 +164,14 @@ __device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX);
 }
 __device__ __forceinline__ float buf_loadf(rsrc_t r, uint32_t off) { return __uint_as_float(buf_load4(r, off)); }
+
+// One agent-coherent 64-bit store of {float bits, tag}: a reader that loads the
+// word with agent-coherent (sc1) loads and sees the current tag has the value
+// (an aligned 8-byte store is seen whole), with no flag and no fence.
+__device__ __forceinline__ void put_tagged(uint64_t* p, float v, unsigned tag) {
+  const uint64_t word = (uint64_t(tag) << 32) | uint64_t(__float_as_uint(v));
+  __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void buf_storef(rsrc_t r, uint32_t off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)off, 0, 0);
 }

@@ -121,11 +121,6 @@ __host__ __device__ inline size_t ws_bytes(int E, int I, int Is, int K) {
   return off;
 }
 
-// One agent-coherent 64-bit store of {value, tag}.
-__device__ __forceinline__ void put_tagged(uint64_t* p, float v, unsigned tag) {
-  const uint64_t word = (uint64_t(tag) << 32) | uint64_t(__float_as_uint(v));
-  __hip_atomic_store(p, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 
 // Loads up to MAXC 16-byte chunks per lane of a row of length n (chunk j of

@@ -11,6 +11,7 @@ import torch
 
 import mega_kernel_qwen36 as mk
 import oracle
+from mega_kernel_qwen36 import _lib
 from tests.inputs import assert_close_out, make_attention, np32
 
 pytestmark = pytest.mark.gpu
@@ -98,3 +99,68 @@ def test_attention_deterministic():
     a = mk.full_attention_decode(inp)
     b = mk.full_attention_decode(inp)
     assert torch.equal(a, b)
+
+
+def _capi_attention(inp, ws):
+    """One call of mkq_full_attention_decode through the C ABI on a caller-owned workspace."""
+    lib = _lib.load_library()
+    b, hq, d = inp.q.shape
+    t, hkv = inp.k_cache.shape[1], inp.k_cache.shape[2]
+    out = torch.empty_like(inp.q)
+    dtype = {torch.bfloat16: _lib.MKQ_DTYPE_BF16, torch.float16: _lib.MKQ_DTYPE_F16}[inp.q.dtype]
+    rc = lib.mkq_full_attention_decode(dtype, inp.q.data_ptr(), inp.k_cache.data_ptr(), inp.v_cache.data_ptr(),
+                                       out.data_ptr(), b, hq, hkv, d, t, inp.scale, ws.data_ptr(), ws.numel(),
+                                       torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.MKQ_OK, lib.mkq_last_error()
+    return out
+
+
+def test_attention_workspace_reuse_across_paths():
+    """One zero-filled workspace, calls of several shapes in turn through the C
+    ABI: the split-K kernels (one workgroup per CU at D = 256, two at 128,
+    several at 40) and the generic kernel (head_dim 20) share it, and every
+    output matches the oracle."""
+    lib = _lib.load_library()
+    shapes = [(1, 24, 4, 256, 32768), (1, 4, 2, 20, 33), (2, 8, 2, 40, 50), (1, 24, 4, 256, 32768),
+              (1, 12, 2, 96, 4500), (1, 24, 4, 256, 1000), (1, 24, 4, 256, 32768)]
+    nbytes = max(lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t) for b, hq, hkv, d, t in shapes)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    inputs = {}
+    for i, key in enumerate(shapes):
+        b, hq, hkv, d, t = key
+        if key not in inputs:
+            inputs[key] = make_attention(batch=b, q_heads=hq, kv_heads=hkv, head_dim=d, seq_len=t, seed=200 + i)
+        inp = inputs[key]
+        out = _capi_attention(inp, ws)
+        torch.cuda.synchronize()
+        assert_close_out(out, _ref(inp))
+
+
+def test_attention_graph_replay():
+    """A captured config-4 call (chunk and merge kernels) replays
+    bit-identically to the eager call; eager calls of two shapes on the same
+    stream, which share the capture's workspace, run between the replays."""
+    inp = make_attention(seq_len=32768, seed=21)
+    eager = mk.full_attention_decode(inp)
+    other = make_attention(batch=1, q_heads=8, kv_heads=2, head_dim=128, seq_len=3000, seed=22)
+    other_ref = mk.full_attention_decode(other)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mk.full_attention_decode(inp)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        res = mk.full_attention_decode(inp)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(res, eager)
+        with torch.cuda.stream(s):
+            mid = mk.full_attention_decode(inp)
+            mid2 = mk.full_attention_decode(other)
+        torch.cuda.synchronize()
+        assert torch.equal(mid, eager)
+        assert torch.equal(mid2, other_ref)
