@@ -44,10 +44,7 @@ constexpr int kTT = 16;                  // tokens per wave tile
 constexpr int kWgTokens = kWaves * kTT;  // tokens per workgroup pass
 constexpr int kMaxD = 256;
 constexpr int kMaxChunks = 1024;
-constexpr int kMergeThreads = 1024;
-constexpr int kMergeSlices = kMergeThreads / kWave;
-constexpr int kMergeBatch = 8;           // chunk loads in flight per merge thread
-static_assert(kMaxChunks <= kMergeThreads, "the merge kernel holds one chunk's (m, l) per thread");
+constexpr int kMergeBatch = 16;          // chunk loads in flight per merge lane
 constexpr uint32_t kFar = 0x80000000u;   // pushes an offset past any descriptor (all < 2^31 bytes)
 constexpr float kNegInf = -INFINITY;
 
@@ -314,66 +311,70 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   }
 }
 
-// grid: (batch * q_heads, ceil(d / 64)); block 1024 = 64 dims x 16 chunk slices.
-// The first batch of partial-O loads is issued before the chunk weights are
-// computed, so both latencies overlap.
+// grid: (batch * q_heads, ceil(d / 64)); block 256.  Lane = output dim; wave
+// w merges chunks [w * cpw, (w + 1) * cpw) online (running max, 16 chunks'
+// partial O loaded per step, their m and l as uniform loads), then the 4
+// waves' (m, l, O) are combined in LDS.  One memory latency per 16 chunks and
+// a single barrier.
 template <typename T>
-__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float* __restrict__ part_o,
-                                                                   const float* __restrict__ part_m,
-                                                                   const float* __restrict__ part_l,
-                                                                   T* __restrict__ out, int d, int nch) {
-  __shared__ float wgt[kMaxChunks];
-  __shared__ float red[kMergeSlices][kWave];
-  __shared__ float rw[2][kMergeSlices];
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __restrict__ part_o,
+                                                              const float* __restrict__ part_m,
+                                                              const float* __restrict__ part_l,
+                                                              T* __restrict__ out, int d, int nch) {
+  __shared__ float so[kWaves][kWave];
+  __shared__ float sml[kWaves][2];
   const int bq = blockIdx.x;
-  const int tid = threadIdx.x, dl = tid % kWave, sl = tid / kWave;
-  const int dim = blockIdx.y * kWave + dl;
+  const int lane = threadIdx.x % kWave, wave = wave_id();
+  const int dim = blockIdx.y * kWave + lane;
+  const int cpw = (nch + kWaves - 1) / kWaves;
+  const int c0 = wave * cpw, c1 = min(nch, c0 + cpw);
   const rsrc_t por = make_rsrc(part_o + size_t(bq) * nch * d, uint32_t(size_t(nch) * d * 4));
   const uint32_t doff = dim < d ? uint32_t(dim) * 4 : kFar;
-  float pv[kMergeBatch];
+  const float* pm = part_m + size_t(bq) * nch;
+  const float* pl = part_l + size_t(bq) * nch;
+  float M = kNegInf, L = 0.f, o = 0.f;
+  for (int cb = c0; cb < c1; cb += kMergeBatch) {
+    float pv[kMergeBatch], mv[kMergeBatch], lv[kMergeBatch];
 #pragma unroll
-  for (int k = 0; k < kMergeBatch; ++k) pv[k] = buf_loadf(por, uint32_t(sl + kMergeSlices * k) * d * 4 + doff);
-  pin_loads();
-
-  // Thread c holds chunk c's (m, l) (nch <= kMaxChunks <= kMergeThreads); both
-  // are loaded with the partial-O batch, so one memory latency covers all.
-  const rsrc_t pmr = make_rsrc(part_m + size_t(bq) * nch, uint32_t(nch) * 4);
-  const rsrc_t plr = make_rsrc(part_l + size_t(bq) * nch, uint32_t(nch) * 4);
-  const float m_ld = buf_loadf(pmr, uint32_t(tid) * 4);
-  const float lc = buf_loadf(plr, uint32_t(tid) * 4);
-  const float mc = tid < nch ? m_ld : kNegInf;
-  float M = wave_max(mc);
-  if (dl == 0) rw[0][sl] = M;
-  __syncthreads();
-  M = rw[0][0];
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const int cc = cb + k;
+      pv[k] = buf_loadf(por, cc < c1 ? uint32_t(cc) * uint32_t(d) * 4u + doff : kFar);
+      const int ci = cc < c1 ? cc : c1 - 1;  // uniform, in range
+      mv[k] = pm[ci];
+      lv[k] = pl[ci];
+    }
+    float mb = M;
 #pragma unroll
-  for (int s = 1; s < kMergeSlices; ++s) M = fmaxf(M, rw[0][s]);
-  const float w = mc == kNegInf ? 0.f : __builtin_amdgcn_exp2f(mc - M);
-  if (tid < nch) wgt[tid] = w;
-  float L = wave_sum(w * lc);
-  if (dl == 0) rw[1][sl] = L;
-  __syncthreads();
-  L = 0.f;
+    for (int k = 0; k < kMergeBatch; ++k) mb = cb + k < c1 ? fmaxf(mb, mv[k]) : mb;
+    const float r = M == kNegInf ? 0.f : __builtin_amdgcn_exp2f(M - mb);
+    o *= r;
+    L *= r;
 #pragma unroll
-  for (int s = 0; s < kMergeSlices; ++s) L += rw[1][s];
-
-  // Chunks past nch loaded zero; their weight index is clamped to a real one.
-  float o = 0.f;
-#pragma unroll
-  for (int k = 0; k < kMergeBatch; ++k) o += wgt[min(sl + kMergeSlices * k, nch - 1)] * pv[k];
-  for (int c0 = kMergeSlices * kMergeBatch; c0 < nch; c0 += kMergeSlices * kMergeBatch) {
-#pragma unroll
-    for (int k = 0; k < kMergeBatch; ++k) pv[k] = buf_loadf(por, uint32_t(c0 + sl + kMergeSlices * k) * d * 4 + doff);
-#pragma unroll
-    for (int k = 0; k < kMergeBatch; ++k) o += wgt[min(c0 + sl + kMergeSlices * k, nch - 1)] * pv[k];
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const float w = cb + k < c1 && mv[k] != kNegInf ? __builtin_amdgcn_exp2f(mv[k] - mb) : 0.f;
+      o += w * pv[k];
+      L += w * lv[k];
+    }
+    M = mb;
   }
-  red[sl][dl] = o;
+  so[wave][lane] = o;
+  if (lane == 0) {
+    sml[wave][0] = M;
+    sml[wave][1] = L;
+  }
   __syncthreads();
-  if (sl == 0 && dim < d) {
-    float s = 0.f;
+  if (wave == 0 && dim < d) {
+    float Mg = kNegInf;
 #pragma unroll
-    for (int k = 0; k < kMergeSlices; ++k) s += red[k][dl];
-    out[size_t(bq) * d + dim] = from_f<T>(s / L);
+    for (int w = 0; w < kWaves; ++w) Mg = fmaxf(Mg, sml[w][0]);
+    float os = 0.f, Ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = sml[w][0] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(sml[w][0] - Mg);
+      os += f * so[w][lane];
+      Ls += f * sml[w][1];
+    }
+    out[size_t(bq) * d + dim] = from_f<T>(os / Ls);
   }
 }
 
@@ -505,7 +506,7 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   MKQ_LAUNCH_CHECK("attn_chunk_kernel");
   if (ch.nch > 1) {
     dim3 g2(batch * hq, (d + kWave - 1) / kWave);
-    attn_merge_kernel<T><<<g2, kMergeThreads, 0, stream>>>(part_o, part_m, part_l, static_cast<T*>(out), d, ch.nch);
+    attn_merge_kernel<T><<<g2, kThreads, 0, stream>>>(part_o, part_m, part_l, static_cast<T*>(out), d, ch.nch);
     MKQ_LAUNCH_CHECK("attn_merge_kernel");
   }
   return MKQ_OK;
