@@ -89,13 +89,25 @@ struct MoeArgs {
   int win_floats;   // act window of the multi-row down phase (floats, a multiple of round_up(I, EPC))
 };
 
+// Every published array (router logits, act, shared act) is written in
+// kCopies copies, one per XCD (workgroup wg runs on XCD wg % 8), each read by
+// that XCD's workgroups only: every workgroup polls the whole array, and 256
+// pollers of one array queue at the few memory channels that hold it.  The
+// copies are an odd number of 256-byte lines apart, so they sit on different
+// channels.  A copy's words are written by lanes 0..kCopies-1 of one store.
+constexpr int kCopies = 8;
+__host__ __device__ inline size_t copy_words(size_t bytes) { return (align256(bytes) + 256) / 8; }
+__host__ __device__ inline size_t logit_copy_words(int E) { return copy_words(8 * size_t(kMaxB) * E); }
+__host__ __device__ inline size_t act_copy_words(int K, int I) { return copy_words(8 * size_t(kMaxB) * K * I); }
+__host__ __device__ inline size_t sact_copy_words(int Is) { return copy_words(8 * size_t(kMaxB) * Is); }
+
 struct WsPtrs {
   unsigned* gen;
   unsigned* err;
   uint64_t* presence;  // [nwg]   tagged
-  uint64_t* logits;  // [B][E]        tagged
-  uint64_t* act;     // [B*K][I]      tagged, (b, slot) rows, route weight folded in
-  uint64_t* sact;    // [B][Is]       tagged
+  uint64_t* logits;  // [kCopies][B][E] tagged, copies logit_copy_words(E) apart
+  uint64_t* act;     // [kCopies][B*K][I] tagged, (b, slot) rows, route weight folded in
+  uint64_t* sact;    // [kCopies][B][Is]  tagged
 };
 
 __host__ __device__ inline WsPtrs ws_ptrs(unsigned char* ws, int E, int I, int Is, int K) {
@@ -105,9 +117,9 @@ __host__ __device__ inline WsPtrs ws_ptrs(unsigned char* ws, int E, int I, int I
   p.presence = reinterpret_cast<uint64_t*>(ws + kOffPresence);
   size_t off = kOffData;
   p.logits = reinterpret_cast<uint64_t*>(ws + off);
-  off = align256(off + 8 * size_t(kMaxB) * E);
+  off = align256(off + 8 * kCopies * logit_copy_words(E));
   p.act = reinterpret_cast<uint64_t*>(ws + off);
-  off = align256(off + 8 * size_t(kMaxB) * K * I);
+  off = align256(off + 8 * kCopies * act_copy_words(K, I));
   p.sact = reinterpret_cast<uint64_t*>(ws + off);
   (void)Is;
   return p;
@@ -115,9 +127,9 @@ __host__ __device__ inline WsPtrs ws_ptrs(unsigned char* ws, int E, int I, int I
 
 __host__ __device__ inline size_t ws_bytes(int E, int I, int Is, int K) {
   size_t off = kOffData;
-  off = align256(off + 8 * size_t(kMaxB) * E);
-  off = align256(off + 8 * size_t(kMaxB) * K * I);
-  off = align256(off + 8 * size_t(kMaxB) * Is);
+  off = align256(off + 8 * kCopies * logit_copy_words(E));
+  off = align256(off + 8 * kCopies * act_copy_words(K, I));
+  off = align256(off + 8 * kCopies * sact_copy_words(Is));
   return off;
 }
 
@@ -624,6 +636,12 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   }
   const unsigned tag = gen + 1u;
   if (tid == 0) put_tagged(w.presence + wg, 0.f, tag);
+  // This XCD's copies of the published act and shared act.  The multi-row
+  // path publishes B times as many act words and keeps one copy: there the
+  // extra stores cost more than the shorter wait saves.
+  constexpr int kActCopies = MB == 1 ? kCopies : 1;
+  uint64_t* const act_r = w.act + (wg % kActCopies) * act_copy_words(K, I);
+  uint64_t* const sact_r = w.sact + (wg % kActCopies) * sact_copy_words(Is);
 
   // Router logits of this wave's rows.  The one-row instance owns at most one
   // router row and one shared row per wave (the host checks E and Is against
@@ -633,13 +651,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   if constexpr (MB == 1) {
     if (e0 < E) {
       const float s = wave_sum_u(dot_row<T, HC>(rrow, xn, H, lane));
-      if (lane == 0) put_tagged(w.logits + e0, s, tag);
+      if (lane < kCopies) put_tagged(w.logits + lane * logit_copy_words(E) + e0, s, tag);
     }
   } else if (wave < B) {
     for (int e = e0, r = 0; e < E; e += rstep, ++r) {
       if (r > 0) load_row<T, VEC, HC>(a.router + size_t(e) * H, H, true, lane, rrow);
       const float s = wave_sum_u(dot_row<T, HC>(rrow, xn + wave * Hp, H, lane));
-      if (lane == 0) put_tagged(w.logits + size_t(wave) * E + e, s, tag);
+      if (lane < kCopies) put_tagged(w.logits + lane * logit_copy_words(E) + size_t(wave) * E + e, s, tag);
     }
   }
   // Shared-expert gate/up of this wave's rows.  The one-row path runs this
@@ -651,7 +669,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         float g = dot_row<T, HC>(sgr, xn, H, lane);
         float u = dot_row<T, HC>(sur, xn, H, lane);
         wave_sum2_u(g, u);
-        if (lane == 0) put_tagged(w.sact + s0, silu(g) * u, tag);
+        if (lane < kActCopies) put_tagged(w.sact + lane * sact_copy_words(Is) + s0, silu(g) * u, tag);
       }
       return;
     }
@@ -664,14 +682,22 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       float g = dot_row<T, HC>(sgr, xn + wave * Hp, H, lane);
       float u = dot_row<T, HC>(sur, xn + wave * Hp, H, lane);
       wave_sum2_u(g, u);
-      if (lane == 0) put_tagged(w.sact + size_t(wave) * Is + s, silu(g) * u, tag);
+      if (lane < kActCopies) put_tagged(w.sact + lane * sact_copy_words(Is) + size_t(wave) * Is + s, silu(g) * u, tag);
     }
   };
   if constexpr (MB > 1) publish_shared();
 
   if constexpr (MB == 1) {
-    issue_shared_gu();
-    issue_shared_down();  // 1 KB per wave, used in phase 3: fetched while HBM idles during the routing
+    // Shared rows (and this wave's 1 KB shared down row, used in phase 3) are
+    // fetched while the logits are exchanged, after the router rows are in --
+    // except by wave 0, which polls for the logits: a wave's loads return in
+    // issue order, so each of its polls would wait for every row issued before
+    // it.  Waves without a shared row issue no placeholder loads (a load past
+    // a descriptor's end reads zero but still takes a memory round trip).
+    if (wave != 0) {
+      if (s0 < Is) issue_shared_gu();
+      issue_shared_down();
+    }
     pin_loads();
     // ---- phases 1-2, one batch row ---------------------------------------------
     // Wave 0 gathers all logits and routes; the other waves wait at the
@@ -687,7 +713,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     if (wave == 0) {
       int my_e;
       float my_w;
-      if (!route_row<EL>(make_rsrc(w.logits, uint32_t(E) * 8u), E, K, tag, lane, my_e, my_w) && lane == 0)
+      if (!route_row<EL>(make_rsrc(w.logits + (wg % kCopies) * logit_copy_words(E), uint32_t(E) * 8u), E, K, tag,
+                         lane, my_e, my_w) &&
+          lane == 0)
         misc[16] = 1;
       if (lane < K) {
         sel_e[lane] = my_e;
@@ -697,6 +725,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
           a.wts[lane] = my_w;
         }
       }
+      if (s0 < Is) issue_shared_gu();
+      issue_shared_down();
+      pin_loads();
     }
     __syncthreads();
     auto slot_expert = [&](int u) { return __builtin_amdgcn_readfirstlane(sel_e[u]); };
@@ -727,7 +758,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
           float gv = dot_row<T, HC>(g[q], xn, H, lane);
           float uv = dot_row<T, HC>(u[q], xn, H, lane);
           wave_sum2_u(gv, uv);
-          if (lane == 0) put_tagged(w.act + size_t(su) * I + i, slot_weight(su) * silu(gv) * uv, tag);
+          if (lane < kActCopies)
+            put_tagged(w.act + lane * act_copy_words(K, I) + size_t(su) * I + i, slot_weight(su) * silu(gv) * uv, tag);
         }
       }
     };
@@ -768,10 +800,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     if constexpr (VEC) {
       const int hpi = Ip / 2, hps = Isp / 2;  // word pairs per row
       ok3 = gather_tagged_pairs(
-          make_rsrc(w.sact, uint32_t(Is) * 8u), hps,
+          make_rsrc(sact_r, uint32_t(Is) * 8u), hps,
           [&](int f) -> uint32_t { return 2 * f < Is ? uint32_t(2 * f) * 8u : 0xFFFFFFF0u; }, sact1, tag, tid);
       ok3 = gather_tagged_pairs(
-                make_rsrc(w.act, uint32_t(K) * uint32_t(I) * 8u), K * hpi,
+                make_rsrc(act_r, uint32_t(K) * uint32_t(I) * 8u), K * hpi,
                 [&](int f) -> uint32_t {
                   const int en = f / hpi, c2 = (f % hpi) * 2;
                   return c2 < I ? uint32_t(en * I + c2) * 8u : 0xFFFFFFF0u;
@@ -785,7 +817,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         const int n = is_sact ? Is : I;
         float val = 0.f;
         if (i < n) {
-          const uint64_t* pw = is_sact ? w.sact + i : w.act + size_t(en) * I + i;
+          const uint64_t* pw = is_sact ? sact_r + i : act_r + size_t(en) * I + i;
           uint64_t word64 = 0;
           for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
             word64 = __hip_atomic_load(const_cast<uint64_t*>(pw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -852,7 +884,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     const int b = wave;
     int my_e;
     float my_w;
-    if (!route_row<EL>(make_rsrc(w.logits + size_t(b) * E, uint32_t(E) * 8u), E, K, tag, lane, my_e, my_w) &&
+    if (!route_row<EL>(make_rsrc(w.logits + (wg % kCopies) * logit_copy_words(E) + size_t(b) * E,
+                                 uint32_t(E) * 8u),
+                       E, K, tag, lane, my_e, my_w) &&
         lane == 0) {
       misc[16] = 1;
       __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -977,9 +1011,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
           if ((mask >> b) & 1u) {
             const float gv = wave_sum_u(dot_row<T, HC>(g[q], xn + b * Hp, H, lane));
             const float uv = wave_sum_u(dot_row<T, HC>(u[q], xn + b * Hp, H, lane));
-            if (lane == 0) {
+            if (lane < kActCopies) {
               const int slot = uslot[ue * MB + b];
-              put_tagged(w.act + (size_t(b) * K + slot) * I + i, sel_w[b * K + slot] * silu(gv) * uv, tag);
+              put_tagged(w.act + lane * act_copy_words(K, I) + (size_t(b) * K + slot) * I + i,
+                         sel_w[b * K + slot] * silu(gv) * uv, tag);
             }
           }
       }
@@ -1015,7 +1050,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // shared act -> LDS [B][Isp]
   bool ok3 = true;
   if constexpr (VEC) {
-    const rsrc_t sr = make_rsrc(w.sact, uint32_t(B) * uint32_t(Is) * 8u);
+    const rsrc_t sr = make_rsrc(sact_r, uint32_t(B) * uint32_t(Is) * 8u);
     const int hp = Isp / 2;  // word pairs per row
     ok3 = gather_tagged_pairs(
         sr, B * hp,
@@ -1031,7 +1066,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       if (i < Is) {
         uint64_t word = 0;
         for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
-          word = __hip_atomic_load(w.sact + size_t(b) * Is + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          word = __hip_atomic_load(sact_r + size_t(b) * Is + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           if (unsigned(word >> 32) == tag) break;
           __builtin_amdgcn_s_sleep(1);
         }
@@ -1064,7 +1099,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       const int e_lo = ent_base[u_lo], ent = ent_base[u_hi] - e_lo;
       __syncthreads();  // previous window (and part[] zeroing) done
       if constexpr (VEC) {
-        const rsrc_t ar = make_rsrc(w.act, uint32_t(B) * uint32_t(K) * uint32_t(I) * 8u);
+        const rsrc_t ar = make_rsrc(act_r, uint32_t(B) * uint32_t(K) * uint32_t(I) * 8u);
         const int hp = Ip / 2;
         ok3 = gather_tagged_pairs(
                   ar, ent * hp,
@@ -1080,7 +1115,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
           float val = 0.f;
           if (i < I) {
             uint64_t word = 0;
-            const uint64_t* pw = w.act + size_t(ent_src[e_lo + en]) * I + i;
+            const uint64_t* pw = act_r + size_t(ent_src[e_lo + en]) * I + i;
             for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
               word = __hip_atomic_load(const_cast<uint64_t*>(pw), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
               if (unsigned(word >> 32) == tag) break;
