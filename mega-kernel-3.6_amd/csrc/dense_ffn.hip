@@ -371,6 +371,7 @@ constexpr int kMaxPairs2 = 2048;     // hidden <= 65536
 constexpr int kPackThreads = 1024;   // K0: one k-step per wave
 constexpr int kPackUnroll = 8;       // K0: x chunks in flight per thread
 constexpr uint32_t kFarOff = 0x80000000u;
+constexpr int kXr = 20;              // k-steps per wave with register-resident x fragments (80 VGPRs)
 
 template <typename T>
 struct MfmaOp;
@@ -566,6 +567,62 @@ __device__ __forceinline__ void pair_mfma(rsrc_t wr, rsrc_t fr, int kdim, int sb
   }
 }
 
+// The same product with the wave's x fragments held in registers: a wave
+// covers at most XR k-steps, so its XR fragments (16 bytes per lane each) are
+// loaded once, before the first weight batch, and the loop streams weights
+// only (each batch used to carry 8 KB of fragment loads per 16 KB of
+// weights).  The batches are unrolled, so every fragment index is a constant.
+template <typename T, int XR>
+__device__ __forceinline__ void pair_mfma_xr(rsrc_t wr, rsrc_t fr, int kdim, int sb, int se, int lane,
+                                             unsigned char* __restrict__ lds, f32x4 (&acc)[2]) {
+  constexpr int NI = kPairRows / 2;
+  constexpr int NB = (XR + kStepBatch - 1) / kStepBatch;
+  const int half = lane >> 5, cb = (lane & 31) * 16;
+  const uint32_t rstride = uint32_t(kdim) * 2u;
+  // Out-of-range steps get kFarOff ORed in (offsets are below 2^31) rather
+  // than selected: in the unrolled batches a select becomes a branch around
+  // each load.
+  auto woff = [&](int s0, int i) -> uint32_t {
+    const int s = s0 + cb / 64;
+    const int k = 32 * s0 + cb / 2;
+    const uint32_t bad = uint32_t(s >= se) | uint32_t(k >= kdim);
+    return (uint32_t(2 * i + half) * rstride + uint32_t(k) * 2u) | (kFarOff * bad);
+  };
+  // Fragments past se are loaded too (no select, so no branch around the
+  // loads): their weights read zero, and past the array they read zero.
+  u32x4 xr[XR];
+#pragma unroll
+  for (int j = 0; j < XR; ++j) xr[j] = buf_load16(fr, (uint32_t(sb + j) * kWave + lane) * 16u);
+  u32x4 wbuf[2][NI];
+  auto issue = [&](int s0, u32x4 (&w)[NI]) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) w[i] = buf_load16<kAuxStream>(wr, woff(s0, i));
+  };
+  unsigned char* wst = lds + (half * kLdsRow + cb);
+  const unsigned char* rd = lds + ((lane & 15) * kLdsRow + 16 * (lane >> 4));
+  acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  issue(sb, wbuf[0]);
+  pin_loads();
+#pragma unroll
+  for (int bt = 0; bt < NB; ++bt) {
+    if (bt + 1 < NB) {
+      issue(sb + (bt + 1) * kStepBatch, wbuf[(bt + 1) & 1]);
+      pin_loads();
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4*>(wst + 2 * i * kLdsRow) = wbuf[bt & 1][i];
+#pragma unroll
+    for (int j = 0; j < kStepBatch; ++j) {
+      if (bt * kStepBatch + j >= XR) break;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(rd + 16 * t * kLdsRow + 64 * j);
+        acc[t] = MfmaOp<T>::mma(a, xr[bt * kStepBatch + j], acc[t]);
+      }
+    }
+  }
+}
+
 // Adds the lo columns (8..15) onto the hi columns (0..7) of an MFMA result:
 // lane l (column l % 16, rows 4 (l / 16) + i) gets the value of lane l + 8.
 __device__ __forceinline__ f32x4 fold_hi_lo(f32x4 a) {
@@ -620,7 +677,7 @@ __device__ __forceinline__ void stash_pair(const f32x4 (&acc)[2], float (*red)[k
 // K1: grid = pairs1 * kSplit1, block 256.  blockIdx = kSplit1 * pair + split;
 // wave w computes matrix (w >> 1: gate, up) over part 2 * split + (w & 1) of
 // 2 * kSplit1 equal parts of k.
-template <typename T>
+template <typename T, int XR>
 __global__ __launch_bounds__(kThreads, 2) void ffn_gateup_mfma_kernel(const T* __restrict__ wg,
                                                                       const T* __restrict__ wu,
                                                                       const uint16_t* __restrict__ xf,
@@ -642,7 +699,10 @@ __global__ __launch_bounds__(kThreads, 2) void ffn_gateup_mfma_kernel(const T* _
   const rsrc_t wr = make_rsrc(w + size_t(r0) * h, uint32_t(rows) * uint32_t(h) * 2u);
   const rsrc_t fr = make_rsrc(xf, uint32_t(s1) * 1024u);
   f32x4 acc[2];
-  pair_mfma<T>(wr, fr, h, sb, se, lane, stage + wave * kWaveLds, acc);
+  if constexpr (XR > 0)
+    pair_mfma_xr<T, XR>(wr, fr, h, sb, se, lane, stage + wave * kWaveLds, acc);
+  else
+    pair_mfma<T>(wr, fr, h, sb, se, lane, stage + wave * kWaveLds, acc);
   stash_pair(acc, red, wave, lane);
   __syncthreads();
   constexpr int kPart = 2 * kPairRows * kMfmaRows;  // floats per (pair, split)
@@ -677,7 +737,7 @@ __global__ __launch_bounds__(kThreads, 2) void ffn_gateup_mfma_kernel(const T* _
 // K2: grid = pairs2 * kSplit2, block 256.  blockIdx = kSplit2 * pair + split;
 // wave w covers part 4 * split + w of 4 * kSplit2 equal parts of k (the
 // intermediate axis).
-template <typename T>
+template <typename T, int XR>
 __global__ __launch_bounds__(kThreads, 2) void ffn_down_mfma_kernel(const T* __restrict__ wd,
                                                                     const uint16_t* __restrict__ af,
                                                                     const T* __restrict__ x, T* __restrict__ out,
@@ -697,7 +757,10 @@ __global__ __launch_bounds__(kThreads, 2) void ffn_down_mfma_kernel(const T* __r
   const rsrc_t wr = make_rsrc(wd + size_t(r0) * inter, uint32_t(rows) * uint32_t(inter) * 2u);
   const rsrc_t fr = make_rsrc(af, uint32_t(s2) * 1024u);
   f32x4 acc[2];
-  pair_mfma<T>(wr, fr, inter, sb, se, lane, stage + wave * kWaveLds, acc);
+  if constexpr (XR > 0)
+    pair_mfma_xr<T, XR>(wr, fr, inter, sb, se, lane, stage + wave * kWaveLds, acc);
+  else
+    pair_mfma<T>(wr, fr, inter, sb, se, lane, stage + wave * kWaveLds, acc);
   stash_pair(acc, red, wave, lane);
   __syncthreads();
   constexpr int kPart = kPairRows * kMfmaRows;
@@ -725,7 +788,7 @@ __global__ __launch_bounds__(kThreads, 2) void ffn_down_mfma_kernel(const T* __r
 template <typename T>
 int launch_mfma(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, T* out, int batch, int h, int inter,
                 float eps, int add_residual, const MfmaWs& ws, hipStream_t stream) {
-  const int s1 = (h + 31) / 32;
+  const int s1 = (h + 31) / 32, s2 = (inter + 31) / 32;
   const int n1 = (inter + kPairRows - 1) / kPairRows, n2 = (h + kPairRows - 1) / kPairRows;
   constexpr int kPackWaves = kPackThreads / kWave;
   for (int b0 = 0; b0 < batch; b0 += kMfmaRows) {
@@ -734,11 +797,16 @@ int launch_mfma(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, 
     ffn_pack_x_kernel<T><<<(s1 + kPackWaves - 1) / kPackWaves, kPackThreads, 0, stream>>>(xb, nw, ws.xf, nb, h, s1,
                                                                                           eps);
     MKQ_LAUNCH_CHECK("ffn_pack_x_kernel");
-    ffn_gateup_mfma_kernel<T><<<kSplit1 * n1, kThreads, 0, stream>>>(wg, wu, ws.xf, ws.af, ws.p1, ws.cnt1, nb, h,
-                                                                     inter);
+    // A wave covers ceil(k-steps / parts) steps at most; up to kXr of them
+    // keep their x fragments in registers.
+    auto* k1 = (s1 + 2 * kSplit1 - 1) / (2 * kSplit1) <= kXr ? ffn_gateup_mfma_kernel<T, kXr>
+                                                              : ffn_gateup_mfma_kernel<T, 0>;
+    k1<<<kSplit1 * n1, kThreads, 0, stream>>>(wg, wu, ws.xf, ws.af, ws.p1, ws.cnt1, nb, h, inter);
     MKQ_LAUNCH_CHECK("ffn_gateup_mfma_kernel");
-    ffn_down_mfma_kernel<T><<<kSplit2 * n2, kThreads, 0, stream>>>(wd, ws.af, xb, out + size_t(b0) * h, ws.p2,
-                                                                   ws.cnt2, nb, h, inter, add_residual);
+    auto* k2 = (s2 + kWaves * kSplit2 - 1) / (kWaves * kSplit2) <= kXr ? ffn_down_mfma_kernel<T, kXr>
+                                                                       : ffn_down_mfma_kernel<T, 0>;
+    k2<<<kSplit2 * n2, kThreads, 0, stream>>>(wd, ws.af, xb, out + size_t(b0) * h, ws.p2, ws.cnt2, nb, h, inter,
+                                              add_residual);
     MKQ_LAUNCH_CHECK("ffn_down_mfma_kernel");
   }
   return MKQ_OK;
