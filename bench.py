@@ -247,6 +247,24 @@ def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
         out[f"attn_t{t}"] = cold
         log(f"attention T={t}: {cold['median_us']:.2f} us cold in stream ({cold['gbps']:.0f} GB/s), "
             f"{cold['warm_median_us']:.2f} us warm, {cold['isolated_event_median_us']:.2f} us isolated launch")
+        if t == 32768:
+            # With cos/sin (rotary_dim 64, one vector pair as the reference
+            # broadcasts): keys rotated inside the kernel, against the
+            # reference's order (rotate the whole cache, then attend).
+            ang = torch.arange(64, dtype=torch.float32, device="cuda") * 0.1
+            rope = mk.FullAttentionInputs(q=inp.q, k_cache=inp.k_cache, v_cache=inp.v_cache,
+                                          cos=torch.cos(ang)[None], sin=torch.sin(ang)[None], rotary_dim=64)
+
+            def rotate_then_attend():
+                qr, kr = mk.ops.apply_partial_rope(rope.q, rope.k_cache, rope.cos, rope.sin, 64)
+                return mk.full_attention_decode(mk.FullAttentionInputs(q=qr, k_cache=kr, v_cache=rope.v_cache))
+
+            for name, f in (("attn_rope_t32768", lambda: mk.full_attention_decode(rope)),
+                            ("attn_rope_python_t32768", rotate_then_attend)):
+                r = measure(timer, f, steps, warmup, attn_bytes(1, 24, 4, 256, t))
+                out[name] = r
+                log(f"attention T={t} with RoPE ({'keys rotated in the kernel' if 'python' not in name else 'cache rotated in torch first'}): "
+                    f"{r['median_us']:.2f} us cold in stream, {r['warm_median_us']:.2f} us warm")
         del inp
         torch.cuda.empty_cache()
     return out

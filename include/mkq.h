@@ -102,6 +102,23 @@ int mkq_full_attention_decode(int dtype, const void* q, const void* k_cache, con
                               int seq_len, float scale, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* The same with q and the keys rotated inside the kernel (rotate-half RoPE
+ * on their first rotary_dim dims, reference.py:91-114).  It replaces the
+ * rotation of q and of the whole k_cache that full_attention_decode
+ * (ops.py:368) runs in Python before _C.full_attention_decode when cos/sin
+ * are given; the reference has no such entry point.  cos_sin: 2 * rotary_dim
+ * floats on the device, cos then sin, the one vector pair the reference
+ * broadcasts over every token and head.  q, k_cache are passed unrotated.
+ * Both are rotated with the reference's rounding (products and sum in FP32,
+ * then dtype), so the result equals the plain entry point on rotated inputs.
+ * rotary_dim: a power of two in [16, head_dim]; bf16/f16, head_dim % 8 == 0
+ * and 16-byte aligned tensors, else MKQ_ERR_UNSUPPORTED.  Uses the same
+ * workspace. */
+int mkq_full_attention_decode_rope(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                                   void* out, int batch, int q_heads, int kv_heads, int head_dim,
+                                   int seq_len, float scale, const float* cos_sin, int rotary_dim,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Recurrent linear-attention decode, reference rule.  Replaces
  *   _C.linear_attention_decode    (csrc/bindings.cpp:35, csrc/linear_attention_decode.cu:46-93)

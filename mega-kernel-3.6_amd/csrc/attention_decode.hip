@@ -75,6 +75,54 @@ struct Mfma<f16_t> {
   static __device__ __forceinline__ _Float16 cvt(float f) { return _Float16(f); }
 };
 
+// 8 floats -> one 16-byte chunk of T (round to nearest even).
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8], bf16_t) {
+  u32x4 r;
+  r.x = uint32_t(f2bf_bits(f[0])) | (uint32_t(f2bf_bits(f[1])) << 16);
+  r.y = uint32_t(f2bf_bits(f[2])) | (uint32_t(f2bf_bits(f[3])) << 16);
+  r.z = uint32_t(f2bf_bits(f[4])) | (uint32_t(f2bf_bits(f[5])) << 16);
+  r.w = uint32_t(f2bf_bits(f[6])) | (uint32_t(f2bf_bits(f[7])) << 16);
+  return r;
+}
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8], f16_t) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f16x2 h;
+    h[0] = _Float16(f[2 * i]);
+    h[1] = _Float16(f[2 * i + 1]);
+    w[i] = __builtin_bit_cast(uint32_t, h);
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Rotate-half RoPE of one 16-byte chunk: x' = x cos + p sin', p = the partner
+// chunk, cos / sin' = 8 values each in LDS (sin' already negated for the
+// lower half).  Two rounded products, a rounded sum, then the rounding to T,
+// as reference.py:91-114's torch ops do: no contraction into an FMA and no
+// fused f32->f16 mixed FMA (the register barriers keep each value FP32).
+template <typename T>
+__device__ __forceinline__ u32x4 rope8(u32x4 xq, u32x4 pq, const float* cs, const float* sn) {
+  float xf[8], pf[8], of[8];
+  unpack(xq, xf, T{});
+  unpack(pq, pf, T{});
+  const f32x4 c0 = reinterpret_cast<const f32x4*>(cs)[0], c1 = reinterpret_cast<const f32x4*>(cs)[1];
+  const f32x4 s0 = reinterpret_cast<const f32x4*>(sn)[0], s1 = reinterpret_cast<const f32x4*>(sn)[1];
+  const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma clang fp contract(off)
+    float a = xf[e] * cv[e];
+    float b = pf[e] * sv[e];
+    asm volatile("" : "+v"(a), "+v"(b));
+    float sum = a + b;
+    asm volatile("" : "+v"(sum));
+    of[e] = sum;
+  }
+  return pack8(of, T{});
+}
+
 // LDS row stride (16-bit elements) of a staged V tile: D/2 dwords padded to
 // 2 mod 8 dwords, so the four token rows 4g+j (g = 0..3) that one transposed
 // read touches start 8 banks apart and cover 32 distinct banks.
@@ -100,11 +148,23 @@ size_t chunk_lds_bytes(int d, int heads) {
 }
 
 // grid: (nchunks * units); block 256.  blockIdx.x = chunk * units + unit.
-template <typename T, int DT>
+//
+// ROPE: the keys are rotated on the fly with the rotate-half rule of
+// reference.py:91-114 and one (cos, sin) vector for every token -- the
+// reference rotates the whole k_cache with the same broadcast vectors before
+// its kernel.  Once a K tile is staged in LDS, its rotary 16-byte chunks are
+// spread over the wave's lanes; each reads its chunk and the partner chunk
+// (dims +-rot/2) and writes the rotated chunk back.  q is rotated the same
+// way once, in registers.  Products and
+// the sum are rounded separately and the result is rounded to T, as the
+// reference's torch ops do, so the rotated q and keys are bit-identical to
+// the reference's.
+template <typename T, int DT, bool ROPE>
 __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, float* __restrict__ part_o,
-    float* __restrict__ part_m, float* __restrict__ part_l, T* __restrict__ out, int hq, int hkv, int d, int seq,
-    int group, int ngroups, int units, int nch, int chunk_tokens, float scale_log2) {
+    float* __restrict__ part_m, float* __restrict__ part_l, T* __restrict__ out, const float* __restrict__ rope_cs,
+    int rot, int rope_lds_off, int hq, int hkv, int d, int seq, int group, int ngroups, int units, int nch,
+    int chunk_tokens, float scale_log2) {
   typedef typename Mfma<T>::vec8 V8;
   typedef typename Mfma<T>::vec4 V4;
   constexpr int NS = DT / 32;               // QK^T MFMA steps over head_dim
@@ -142,6 +202,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const int d0 = 32 * s + 8 * grp;
     qop[s] = __builtin_bit_cast(V8, buf_load16(qr, d0 < d ? uint32_t(col * d + d0) * uint32_t(sizeof(T)) : kFar));
   }
+  // ROPE: q's partner chunks (dims +-rot/2) and this thread's cos/sin values
+  // are loaded here, before the K/V stream, and used after it is issued.
+  u32x4 qpart[NS];
+  float cs_ld[2] = {0.f, 0.f};
+  if constexpr (ROPE) {
+    const int half = rot / 2;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int d0 = 32 * s + 8 * grp;
+      const int pd = d0 < half ? d0 + half : d0 - half;
+      qpart[s] = buf_load16(qr, d0 < rot ? uint32_t(col * d + pd) * uint32_t(sizeof(T)) : kFar);
+    }
+    const rsrc_t cr = make_rsrc(rope_cs, uint32_t(2 * rot) * 4u);
+    cs_ld[0] = buf_loadf(cr, uint32_t(threadIdx.x) * 4u);
+    cs_ld[1] = buf_loadf(cr, uint32_t(threadIdx.x + kThreads) * 4u);
+  }
   // K and V chunk i of a tile: token row qi / CPR, dims 8 * (qi % CPR),
   // qi = lane + 64 i (two 512-byte token rows per load at D = 256).
   uint32_t voff[VCH];
@@ -151,6 +227,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const int row = qi / CPR, dc = qi % CPR;
     voff[i] = uint32_t(row) * tsb + (dc * 8 < d ? uint32_t(dc * 16) : kFar);
   }
+  // ROPE: cos and the signed sin (rotate_half negates the upper half) of the
+  // rotary dims, in LDS after the staging/merge area.
+  const int rhc = ROPE ? rot / 16 : 0;  // partner chunk distance
+  float* rope_l = reinterpret_cast<float*>(smem + rope_lds_off);
+  static_assert(2 * kMaxD <= 2 * kThreads, "two cos/sin values per thread fill the table");
   unsigned char* stage = smem + size_t(wave) * stage_bytes(DT);
   uint16_t* vt = reinterpret_cast<uint16_t*>(stage);
   constexpr int KSTR = k_stride_bytes(DT);
@@ -168,6 +249,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, uint32_t(t0) * tsb + voff[i]);
   pin_loads();
 
+  // ROPE, once the first tile is in flight: the cos/sin table into LDS, then
+  // q's rotary chunks rotated in place (q' = q cos + rotate_half(q) sin, the
+  // same rounding as the keys); q's loads were issued before K/V, so this
+  // waits for them alone.
+  if constexpr (ROPE) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = threadIdx.x + j * kThreads;
+      if (t < 2 * rot) rope_l[t] = t >= rot && t < rot + rot / 2 ? -cs_ld[j] : cs_ld[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int d0 = 32 * s + 8 * grp;
+      if (d0 < rot) qop[s] = __builtin_bit_cast(V8, rope8<T>(__builtin_bit_cast(u32x4, qop[s]), qpart[s],
+                                                             rope_l + d0, rope_l + rot + d0));
+    }
+  }
+
   // One 16-token tile whose K and V are in kreg/vreg; with `pf` the next
   // pass's tile is prefetched into them.  The last tile prefetches nothing:
   // loads past the chunk read zero but still take a memory round trip, which
@@ -179,6 +279,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     for (int i = 0; i < VCH; ++i) {
       const int qi = lane + kWave * i;
       *reinterpret_cast<u32x4*>(stage + (qi / CPR) * KSTR + (qi % CPR) * 16) = kreg[i];
+    }
+    if constexpr (ROPE) {
+      // Rotary chunks, k' = k cos + rotate_half(k) sin: the tile's 16 * rot/8
+      // of them spread over the wave's lanes (chunk j = row j / nrc, chunk
+      // j % nrc).  A chunk and its partner (j ^ rhc) fall in the same group of
+      // 64, so both lanes read before either writes, and groups are whole
+      // rows.
+      const int nrc = rot / 8;
+      for (int j = lane; j < kTT * nrc; j += kWave) {
+        unsigned char* rowp = stage + (j / nrc) * KSTR;
+        const int c = j % nrc;
+        const u32x4 own = *reinterpret_cast<const u32x4*>(rowp + c * 16);
+        const u32x4 pq = *reinterpret_cast<const u32x4*>(rowp + (c ^ rhc) * 16);
+        *reinterpret_cast<u32x4*>(rowp + c * 16) = rope8<T>(own, pq, rope_l + c * 8, rope_l + rot + c * 8);
+      }
     }
     const uint32_t next = uint32_t(t0 + kWgTokens) * tsb;
     if (pf) {
@@ -481,7 +596,7 @@ size_t fast_ws_floats(int batch, int hq, int d, int seq) { return size_t(batch) 
 
 template <typename T, int DT>
 int launch_fast(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
-                float scale, float* ws, hipStream_t stream) {
+                float scale, const float* rope_cs, int rot, float* ws, hipStream_t stream) {
   const int group = hq / hkv;
   const int ngroups = (group + 15) / 16;
   const int units = batch * hkv * ngroups;
@@ -491,18 +606,25 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   const size_t lds = chunk_lds_bytes<DT>(d, group < 16 ? group : 16);
   static bool attr_set = false;
   if (!attr_set) {
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT>),
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     int(chunk_lds_bytes<DT>(DT, 16))));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    int(chunk_lds_bytes<DT>(DT, 16) + 16 + 2 * kMaxD * sizeof(float))));
     attr_set = true;
   }
   MKQ_REQUIRE(size_t(ch.nch) * units < (size_t(1) << 31), "full_attention_decode: grid too large");
   float* part_o = ws;
   float* part_m = part_o + size_t(batch) * hq * ch.nch * d;
   float* part_l = part_m + size_t(batch) * hq * ch.nch;
-  attn_chunk_kernel<T, DT><<<dim3(ch.nch * units), kThreads, lds, stream>>>(
+  auto* kern = rot > 0 ? attn_chunk_kernel<T, DT, true> : attn_chunk_kernel<T, DT, false>;
+  const size_t rope_off = (lds + 15) / 16 * 16;  // the cos/sin table follows the staging/merge area
+  const size_t lds_all = rot > 0 ? rope_off + size_t(2 * rot) * sizeof(float) : lds;
+  kern<<<dim3(ch.nch * units), kThreads, lds_all, stream>>>(
       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), part_o, part_m, part_l,
-      static_cast<T*>(out), hq, hkv, d, seq, group, ngroups, units, ch.nch, ch.chunk_tokens, scale * kLog2e);
+      static_cast<T*>(out), rope_cs, rot, int(rope_off), hq, hkv, d, seq, group, ngroups, units, ch.nch,
+      ch.chunk_tokens, scale * kLog2e);
   MKQ_LAUNCH_CHECK("attn_chunk_kernel");
   if (ch.nch > 1) {
     dim3 g2(batch * hq, (d + kWave - 1) / kWave);
@@ -514,10 +636,10 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
 
 template <typename T>
 int launch_fast_d(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
-                  float scale, float* ws, hipStream_t stream) {
-  if (d <= 64) return launch_fast<T, 64>(q, k, v, out, batch, hq, hkv, d, seq, scale, ws, stream);
-  if (d <= 128) return launch_fast<T, 128>(q, k, v, out, batch, hq, hkv, d, seq, scale, ws, stream);
-  return launch_fast<T, 256>(q, k, v, out, batch, hq, hkv, d, seq, scale, ws, stream);
+                  float scale, const float* rope_cs, int rot, float* ws, hipStream_t stream) {
+  if (d <= 64) return launch_fast<T, 64>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ws, stream);
+  if (d <= 128) return launch_fast<T, 128>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ws, stream);
+  return launch_fast<T, 256>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ws, stream);
 }
 
 template <typename T>
@@ -542,39 +664,66 @@ extern "C" size_t mkq_full_attention_decode_workspace_bytes(int batch, int q_hea
   return sizeof(float) * (fast > generic ? fast : generic);
 }
 
-extern "C" int mkq_full_attention_decode(int dtype, const void* q, const void* k_cache, const void* v_cache,
-                                         void* out, int batch, int q_heads, int kv_heads, int head_dim, int seq_len,
-                                         float scale, void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+int attention_entry(const char* fn, int dtype, const void* q, const void* k_cache, const void* v_cache, void* out,
+                    int batch, int q_heads, int kv_heads, int head_dim, int seq_len, float scale,
+                    const float* rope_cs, int rot, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
-  MKQ_REQUIRE(batch > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0, "full_attention_decode: sizes must be positive");
+  MKQ_REQUIRE(batch > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0, "%s: sizes must be positive", fn);
   MKQ_REQUIRE(seq_len > 0, "seq_len must be positive");
   MKQ_REQUIRE(q_heads % kv_heads == 0, "query_heads must be divisible by kv_heads");
   MKQ_REQUIRE(head_dim <= kMaxD, "head_dim > 256 is not supported by this kernel");
-  MKQ_REQUIRE(q && k_cache && v_cache && out, "full_attention_decode: null tensor pointer");
-  MKQ_REQUIRE(batch <= 65535 && q_heads <= 65535, "full_attention_decode: batch/heads too large");
+  MKQ_REQUIRE(q && k_cache && v_cache && out, "%s: null tensor pointer", fn);
+  MKQ_REQUIRE(batch <= 65535 && q_heads <= 65535, "%s: batch/heads too large", fn);
   MKQ_REQUIRE(workspace && workspace_bytes >= mkq_full_attention_decode_workspace_bytes(batch, q_heads, kv_heads,
                                                                                         head_dim, seq_len),
-              "full_attention_decode: workspace too small");
-  MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0,
-              "full_attention_decode: workspace must be 256-byte aligned");
+              "%s: workspace too small", fn);
+  MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "%s: workspace must be 256-byte aligned", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* ws = static_cast<float*>(workspace);
   const bool fast_ok = (head_dim % 8 == 0) && aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
+  if (rot > 0) {
+    MKQ_REQUIRE(rope_cs, "%s: null cos/sin pointer", fn);
+    if (!fast_ok || (dtype != MKQ_DTYPE_BF16 && dtype != MKQ_DTYPE_F16) || rot < 16 || rot > head_dim ||
+        (rot & (rot - 1)) != 0)
+      return set_error(MKQ_ERR_UNSUPPORTED,
+                       "%s: rotary_dim %d needs a power of two in [16, head_dim], bf16/f16 and head_dim %% 8 == 0 "
+                       "with 16-byte aligned tensors",
+                       fn, rot);
+  }
   switch (dtype) {
     case MKQ_DTYPE_BF16:
       return fast_ok ? launch_fast_d<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                             scale, ws, s)
+                                             scale, rope_cs, rot, ws, s)
                      : launch_generic<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                               scale, ws, s);
     case MKQ_DTYPE_F16:
       return fast_ok ? launch_fast_d<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                            scale, ws, s)
+                                            scale, rope_cs, rot, ws, s)
                      : launch_generic<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                              scale, ws, s);
     case MKQ_DTYPE_F32:
       return launch_generic<float>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len, scale, ws,
                                    s);
     default:
-      return set_error(MKQ_ERR_INVALID, "full_attention_decode: unknown dtype %d", dtype);
+      return set_error(MKQ_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
   }
+}
+
+}  // namespace
+
+extern "C" int mkq_full_attention_decode(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                                         void* out, int batch, int q_heads, int kv_heads, int head_dim, int seq_len,
+                                         float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  return attention_entry("full_attention_decode", dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads,
+                         head_dim, seq_len, scale, nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mkq_full_attention_decode_rope(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                                              void* out, int batch, int q_heads, int kv_heads, int head_dim,
+                                              int seq_len, float scale, const float* cos_sin, int rotary_dim,
+                                              void* workspace, size_t workspace_bytes, void* stream) {
+  return attention_entry("full_attention_decode_rope", dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads,
+                         head_dim, seq_len, scale, cos_sin, rotary_dim, workspace, workspace_bytes, stream);
 }

@@ -197,7 +197,8 @@ torch::Tensor dense_ffn_decode(torch::Tensor x, torch::Tensor norm_weight, torch
   return out;
 }
 
-torch::Tensor full_attention_decode(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, double scale) {
+torch::Tensor attention_impl(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, double scale,
+                             const torch::Tensor* cos_sin, int64_t rotary_dim) {
   // Checks and messages as in attention_decode.cu:157-175.
   MK_CHECK_INPUT(q);
   MK_CHECK_INPUT(k_cache);
@@ -220,12 +221,33 @@ torch::Tensor full_attention_decode(torch::Tensor q, torch::Tensor k_cache, torc
   c10::DeviceGuard guard(q.device());
   auto out = torch::empty_like(q);
   auto ws = workspace_for(Ws::kAttention, q, mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq_len));
-  const int rc = mkq_full_attention_decode(to_mkq_dtype(q), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                                           out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq_len,
-                                           static_cast<float>(scale), ws.data_ptr(), static_cast<size_t>(ws.numel()),
-                                           current_stream());
-  check_status(rc, "full_attention_decode");
+  int rc;
+  if (cos_sin == nullptr) {
+    rc = mkq_full_attention_decode(to_mkq_dtype(q), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                   out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq_len,
+                                   static_cast<float>(scale), ws.data_ptr(), static_cast<size_t>(ws.numel()),
+                                   current_stream());
+  } else {
+    TORCH_CHECK(cos_sin->is_cuda() && cos_sin->is_contiguous() && cos_sin->scalar_type() == torch::kFloat32,
+                "cos_sin must be a contiguous float32 device tensor");
+    TORCH_CHECK(cos_sin->numel() == 2 * rotary_dim, "cos_sin must hold 2 * rotary_dim values");
+    rc = mkq_full_attention_decode_rope(to_mkq_dtype(q), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                        out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq_len,
+                                        static_cast<float>(scale), cos_sin->data_ptr<float>(),
+                                        static_cast<int>(rotary_dim), ws.data_ptr(),
+                                        static_cast<size_t>(ws.numel()), current_stream());
+  }
+  check_status(rc, cos_sin == nullptr ? "full_attention_decode" : "full_attention_decode_rope");
   return out;
+}
+
+torch::Tensor full_attention_decode(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, double scale) {
+  return attention_impl(q, k_cache, v_cache, scale, nullptr, 0);
+}
+
+torch::Tensor full_attention_decode_rope(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, double scale,
+                                         torch::Tensor cos_sin, int64_t rotary_dim) {
+  return attention_impl(q, k_cache, v_cache, scale, &cos_sin, rotary_dim);
 }
 
 std::tuple<torch::Tensor, torch::Tensor> linear_attention_decode(torch::Tensor q, torch::Tensor k, torch::Tensor v,
@@ -348,6 +370,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Persistent MoE decode with a sigmoid-gated shared expert (HIP)");
   m.def("dense_ffn_decode", &dense_ffn_decode, "Fused RMSNorm + SwiGLU FFN decode (HIP)");
   m.def("full_attention_decode", &full_attention_decode, "Split-K GQA flash-decode (HIP)");
+  m.def("full_attention_decode_rope", &full_attention_decode_rope,
+        "Split-K GQA flash-decode with the keys rotated on the fly (HIP)");
   m.def("linear_attention_decode", &linear_attention_decode, "Recurrent linear-attention decode (HIP)");
   m.def("gated_delta_decode", &gated_delta_decode, "Gated delta rule decode (HIP)");
   m.def("gated_delta_decode_", &gated_delta_decode_, "Gated delta rule decode, state updated in place (HIP)");

@@ -27,6 +27,7 @@ Differences from the reference, all deliberate:
 from __future__ import annotations
 
 import math
+import weakref
 from dataclasses import dataclass
 from typing import Optional
 
@@ -257,34 +258,77 @@ def dense_ffn_decode(
     return _C.dense_ffn_decode(*tensors, float(eps), bool(add_residual))
 
 
+def _rope_one(t, cos, sin, rotary_dim: int):
+    """Rotate-half RoPE of one tensor; cos/sin FP32, broadcast over its leading dims."""
+    half = rotary_dim // 2
+    tr = t[..., :rotary_dim].float()
+    rh = torch.cat((-tr[..., half:], tr[..., :half]), dim=-1)
+    c, s = cos, sin
+    while c.ndim < tr.ndim:
+        c, s = c.unsqueeze(0), s.unsqueeze(0)
+    return torch.cat(((tr * c + rh * s).to(t.dtype), t[..., rotary_dim:]), dim=-1)
+
+
 def apply_partial_rope(q, k, cos, sin, rotary_dim: int):
     """Rotate-half RoPE on the first ``rotary_dim`` dims of q and k (reference.py:91-114)."""
     if cos is None or sin is None or rotary_dim <= 0:
         return q, k
-    half = rotary_dim // 2
     cos = cos.to(device=q.device, dtype=torch.float32)
     sin = sin.to(device=q.device, dtype=torch.float32)
+    return _rope_one(q, cos, sin, rotary_dim), _rope_one(k, cos, sin, rotary_dim)
 
-    def rotate(t):
-        tr = t[..., :rotary_dim].float()
-        rh = torch.cat((-tr[..., half:], tr[..., :half]), dim=-1)
-        c, s = cos, sin
-        while c.ndim < tr.ndim:
-            c, s = c.unsqueeze(0), s.unsqueeze(0)
-        return torch.cat(((tr * c + rh * s).to(t.dtype), t[..., rotary_dim:]), dim=-1)
 
-    return rotate(q), rotate(k)
+# Last (cos, sin) vector built for the kernel: weak references to the source
+# tensors and their version counters, so a tensor that is modified in place,
+# replaced or freed is never matched.
+_ROPE_CS_CACHE: dict = {}
+
+
+def _rope_in_kernel(inputs: FullAttentionInputs) -> Optional[torch.Tensor]:
+    """The (cos, sin) pair as one device vector when the kernel can rotate the
+    keys itself: one vector for every token and head (what the reference
+    broadcasts), a power-of-two rotary_dim in [16, head_dim], bf16/f16 and a
+    head_dim that is a multiple of 8.  None otherwise."""
+    cos, sin, rot = inputs.cos, inputs.sin, inputs.rotary_dim
+    k = inputs.k_cache
+    d = k.shape[-1]
+    if cos is None or sin is None or rot <= 0:
+        return None
+    if cos.numel() != rot or sin.numel() != rot or rot < 16 or rot > d or rot & (rot - 1) or d % 8:
+        return None
+    if k.dtype not in (torch.bfloat16, torch.float16) or not k.is_cuda:
+        return None
+    c = _ROPE_CS_CACHE
+    versions = (cos._version, sin._version)
+    if c and c["cos"]() is cos and c["sin"]() is sin and c["versions"] == versions and c["device"] == k.device:
+        return c["cs"]
+    cs = torch.cat((cos.reshape(-1), sin.reshape(-1))).to(device=k.device, dtype=torch.float32).contiguous()
+    c.update(cos=weakref.ref(cos), sin=weakref.ref(sin), versions=versions, device=k.device, cs=cs)
+    return cs
 
 
 def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:
-    """One-token GQA attention over a contiguous KV cache (split-K flash-decode, HIP)."""
-    q, k_cache = apply_partial_rope(inputs.q, inputs.k_cache, inputs.cos, inputs.sin, inputs.rotary_dim)
+    """One-token GQA attention over a contiguous KV cache (split-K flash-decode, HIP).
+
+    With cos/sin, the reference rotates q and the whole k_cache before its
+    kernel (ops.py:368).  Here, where the kernel supports it, q and the keys
+    are rotated inside the kernel as the keys stream, with the same rounding;
+    otherwise both are rotated first, as the reference does.  Device-resident
+    cos/sin avoid a host-to-device copy per call."""
+    cs = _rope_in_kernel(inputs)
+    if cs is not None:
+        q, k_cache = inputs.q, inputs.k_cache  # both rotated inside the kernel
+    else:
+        q, k_cache = apply_partial_rope(inputs.q, inputs.k_cache, inputs.cos, inputs.sin, inputs.rotary_dim)
     scale = inputs.scale
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     if q.shape[1] % k_cache.shape[2] != 0:
         raise ValueError("query_heads must be divisible by kv_heads")
     _require_extension("full_attention_decode", q, k_cache, inputs.v_cache)
+    if cs is not None:
+        return _C.full_attention_decode_rope(q.contiguous(), k_cache.contiguous(), inputs.v_cache.contiguous(),
+                                             float(scale), cs, int(inputs.rotary_dim))
     return _C.full_attention_decode(q.contiguous(), k_cache.contiguous(), inputs.v_cache.contiguous(), float(scale))
 
 

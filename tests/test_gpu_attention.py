@@ -164,3 +164,63 @@ def test_attention_graph_replay():
         torch.cuda.synchronize()
         assert torch.equal(mid, eager)
         assert torch.equal(mid2, other_ref)
+
+
+def _rope_inputs(shape, rot, seed, dtype=torch.bfloat16):
+    b, hq, hkv, d, t = shape
+    inp = make_attention(batch=b, q_heads=hq, kv_heads=hkv, head_dim=d, seq_len=t, seed=seed, dtype=dtype)
+    g = torch.Generator().manual_seed(seed + 1)
+    ang = torch.rand(rot, generator=g) * 6.0
+    cos, sin = torch.cos(ang)[None], torch.sin(ang)[None]  # one vector for every token, as the reference broadcasts
+    return inp, cos, sin
+
+
+@pytest.mark.parametrize("shape,rot,dtype", [
+    ((1, 24, 4, 256, 4096), 64, torch.bfloat16),
+    ((2, 8, 2, 128, 300), 32, torch.bfloat16),
+    ((1, 8, 8, 64, 77), 64, torch.bfloat16),       # rotary_dim == head_dim
+    ((1, 12, 2, 128, 2000), 16, torch.float16),
+    ((1, 24, 4, 256, 65), 128, torch.bfloat16),
+])
+def test_attention_rope_in_kernel_equals_rotated_cache(shape, rot, dtype):
+    """Keys rotated inside the kernel give exactly the output of the plain
+    kernel on a cache rotated beforehand (the reference's order,
+    reference.py:91-114 then attention_decode.cu), and match the oracle."""
+    inp, cos, sin = _rope_inputs(shape, rot, seed=300 + sum(shape) + rot, dtype=dtype)
+    fused = mk.full_attention_decode(mk.FullAttentionInputs(q=inp.q, k_cache=inp.k_cache, v_cache=inp.v_cache,
+                                                            cos=cos, sin=sin, rotary_dim=rot))
+    qr, kr = mk.ops.apply_partial_rope(inp.q, inp.k_cache, cos, sin, rot)
+    plain = mk.full_attention_decode(mk.FullAttentionInputs(q=qr, k_cache=kr, v_cache=inp.v_cache))
+    assert torch.equal(fused, plain)
+    qn, kn = oracle.apply_partial_rope(np32(inp.q), np32(inp.k_cache), cos.numpy(), sin.numpy(), rot)
+    qn, kn = oracle.bf16_round(qn), oracle.bf16_round(kn)
+    if dtype == torch.bfloat16:
+        assert_close_out(fused, oracle.full_attention_decode(qn, kn, np32(inp.v_cache),
+                                                             scale=1.0 / math.sqrt(shape[3])))
+
+
+def test_attention_rope_fallback_rotates_the_cache():
+    """A rotary_dim the kernel does not rotate (24) still follows the
+    reference: the cache is rotated first, then the plain kernel runs."""
+    inp, cos, sin = _rope_inputs((1, 8, 2, 64, 200), 24, seed=401)
+    out = mk.full_attention_decode(mk.FullAttentionInputs(q=inp.q, k_cache=inp.k_cache, v_cache=inp.v_cache,
+                                                          cos=cos, sin=sin, rotary_dim=24))
+    qn, kn = oracle.apply_partial_rope(np32(inp.q), np32(inp.k_cache), cos.numpy(), sin.numpy(), 24)
+    qn, kn = oracle.bf16_round(qn), oracle.bf16_round(kn)
+    assert_close_out(out, oracle.full_attention_decode(qn, kn, np32(inp.v_cache), scale=1.0 / math.sqrt(64)))
+
+
+def test_attention_rope_cos_changed_in_place():
+    """The device (cos, sin) vector built for the kernel is reused only while
+    the same cos/sin tensors are unchanged: an in-place update is seen."""
+    inp, cos, sin = _rope_inputs((1, 8, 2, 128, 500), 64, seed=501)
+    cos, sin = cos.cuda(), sin.cuda()
+    full = mk.FullAttentionInputs(q=inp.q, k_cache=inp.k_cache, v_cache=inp.v_cache, cos=cos, sin=sin, rotary_dim=64)
+    first = mk.full_attention_decode(full)
+    cos.mul_(-0.5)
+    sin.add_(0.25)
+    second = mk.full_attention_decode(full)
+    qr, kr = mk.ops.apply_partial_rope(inp.q, inp.k_cache, cos, sin, 64)
+    plain = mk.full_attention_decode(mk.FullAttentionInputs(q=qr, k_cache=kr, v_cache=inp.v_cache))
+    assert torch.equal(second, plain)
+    assert not torch.equal(first, second)

@@ -61,6 +61,31 @@ def test_c_abi_rejects_bad_arguments_without_gpu():
     assert b"multiple of k_heads" in lib.mkq_last_error()
 
 
+def test_rope_entry_rejects_unsupported_rotary_dims_without_gpu():
+    """The in-kernel RoPE entry point validates on the host and returns
+    MKQ_ERR_UNSUPPORTED for rotary dims it cannot rotate in the kernel; the
+    buffers are host memory and are never touched."""
+    lib = _lib.load_library()
+    b, hq, hkv, d, t = 1, 4, 2, 64, 8
+    nbytes = lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t)
+    raw = ctypes.create_string_buffer(nbytes + 512)
+    ws = (ctypes.addressof(raw) + 255) // 256 * 256
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    for rot in (24, 8, 128):
+        rc = lib.mkq_full_attention_decode_rope(_lib.MKQ_DTYPE_BF16, p16, p16, p16, p16, b, hq, hkv, d, t, 1.0, p16,
+                                                rot, ws, nbytes, None)
+        assert rc == _lib.MKQ_ERR_UNSUPPORTED, rot
+        assert b"rotary_dim" in lib.mkq_last_error()
+    rc = lib.mkq_full_attention_decode_rope(_lib.MKQ_DTYPE_F32, p16, p16, p16, p16, b, hq, hkv, d, t, 1.0, p16, 32,
+                                            ws, nbytes, None)
+    assert rc == _lib.MKQ_ERR_UNSUPPORTED
+    rc = lib.mkq_full_attention_decode_rope(_lib.MKQ_DTYPE_BF16, p16, p16, p16, p16, b, hq, hkv, d, t, 1.0, None, 32,
+                                            ws, nbytes, None)
+    assert rc == _lib.MKQ_ERR_INVALID
+    assert b"null cos/sin pointer" in lib.mkq_last_error()
+
+
 def test_workspace_sizes():
     lib = _lib.load_library()
     # act [batch, intermediate] FP32 plus the batched path's fragments, partials and counters
