@@ -153,6 +153,18 @@ int mkq_gated_delta_decode(int dtype, const void* q, const void* k, const void* 
 int mkq_gemv(int dtype, const void* x, const void* w, const void* residual, void* y, int batch,
              int in_features, int out_features, void* stream);
 
+/* ------------------------------------------------------------------------
+ * The same GEMV with the residual add of decode_layer fused in:
+ *   y[b, n]   = round(sum_k w[n, k] * x[b, k])
+ *   sum[b, n] = round(residual[b, n] + y[b, n])
+ * Both outputs carry the roundings of the reference's separate add
+ * `residual = residual + attention_output` (ops.py:722-723, 728-729), so
+ * sum is bit-identical to that add applied to y.  No counterpart in the
+ * reference.  residual, y and sum must not alias.
+ * ---------------------------------------------------------------------- */
+int mkq_gemv_add(int dtype, const void* x, const void* w, const void* residual, void* y, void* sum,
+                 int batch, int in_features, int out_features, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,8 @@
 // Small-batch GEMV y[b, n] = sum_k w[n, k] x[b, k] (+ residual[b, n]) for the
 // optional attention output projections of decode_layer.  x is staged in LDS
-// as FP32; each wave streams whole weight rows with 128-bit loads.
+// as FP32; each wave streams whole weight rows with 128-bit loads.  The
+// two-output form also writes sum[b, n] = residual[b, n] + y[b, n] with y
+// rounded to T first, the same two roundings as a separate elementwise add.
 #include "mkq_host.h"
 
 using namespace mkq;
@@ -14,8 +16,8 @@ constexpr int kUnroll = 4;
 
 template <typename T, int NB, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x, const T* __restrict__ w,
-                                                        const T* __restrict__ residual, T* __restrict__ y, int kdim,
-                                                        int n, int rows_per_wg) {
+                                                        const T* __restrict__ residual, T* __restrict__ y,
+                                                        T* __restrict__ sum, int kdim, int n, int rows_per_wg) {
   constexpr int EPC = Epc<T>::value;
   extern __shared__ float xs[];
   const int kp = (kdim + EPC - 1) / EPC * EPC;
@@ -54,14 +56,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x,
       const float s = wave_sum(acc[b]);
       if (lane == 0) {
         const size_t o = size_t(b) * n + r;
-        y[o] = from_f<T>(residual ? s + to_f(residual[o]) : s);
+        if (sum) {
+          const T yv = from_f<T>(s);
+          y[o] = yv;
+          sum[o] = from_f<T>(to_f(residual[o]) + to_f(yv));
+        } else {
+          y[o] = from_f<T>(residual ? s + to_f(residual[o]) : s);
+        }
       }
     }
   }
 }
 
 template <typename T, int NB>
-int launch(const T* x, const T* w, const T* residual, T* y, int kdim, int n, hipStream_t stream) {
+int launch(const T* x, const T* w, const T* residual, T* y, T* sum, int kdim, int n, hipStream_t stream) {
   constexpr int EPC = Epc<T>::value;
   const size_t lds = sizeof(float) * NB * size_t((kdim + EPC - 1) / EPC * EPC);
   if (lds > size_t(max_lds_per_block()))
@@ -78,31 +86,33 @@ int launch(const T* x, const T* w, const T* residual, T* y, int kdim, int n, hip
   const int rows = 2 * kWaves;
   const int grid = (n + rows - 1) / rows;
   if (vec)
-    gemv_kernel<T, NB, true><<<grid, kThreads, lds, stream>>>(x, w, residual, y, kdim, n, rows);
+    gemv_kernel<T, NB, true><<<grid, kThreads, lds, stream>>>(x, w, residual, y, sum, kdim, n, rows);
   else
-    gemv_kernel<T, NB, false><<<grid, kThreads, lds, stream>>>(x, w, residual, y, kdim, n, rows);
+    gemv_kernel<T, NB, false><<<grid, kThreads, lds, stream>>>(x, w, residual, y, sum, kdim, n, rows);
   MKQ_LAUNCH_CHECK("gemv_kernel");
   return MKQ_OK;
 }
 
 template <typename T>
-int gemv_typed(const void* xv, const void* wv, const void* rv, void* yv, int batch, int kdim, int n,
+int gemv_typed(const void* xv, const void* wv, const void* rv, void* yv, void* sv, int batch, int kdim, int n,
                hipStream_t stream) {
   const T* x = static_cast<const T*>(xv);
   const T* w = static_cast<const T*>(wv);
   const T* r = static_cast<const T*>(rv);
   T* y = static_cast<T*>(yv);
+  T* sm = static_cast<T*>(sv);
   for (int b0 = 0; b0 < batch; b0 += kMaxNb) {
     const int nb = batch - b0 < kMaxNb ? batch - b0 : kMaxNb;
     const T* xb = x + size_t(b0) * kdim;
     const T* rb = r ? r + size_t(b0) * n : nullptr;
     T* yb = y + size_t(b0) * n;
+    T* sb = sm ? sm + size_t(b0) * n : nullptr;
     int rc;
     switch (nb) {
-      case 1: rc = launch<T, 1>(xb, w, rb, yb, kdim, n, stream); break;
-      case 2: rc = launch<T, 2>(xb, w, rb, yb, kdim, n, stream); break;
-      case 3: rc = launch<T, 3>(xb, w, rb, yb, kdim, n, stream); break;
-      default: rc = launch<T, 4>(xb, w, rb, yb, kdim, n, stream); break;
+      case 1: rc = launch<T, 1>(xb, w, rb, yb, sb, kdim, n, stream); break;
+      case 2: rc = launch<T, 2>(xb, w, rb, yb, sb, kdim, n, stream); break;
+      case 3: rc = launch<T, 3>(xb, w, rb, yb, sb, kdim, n, stream); break;
+      default: rc = launch<T, 4>(xb, w, rb, yb, sb, kdim, n, stream); break;
     }
     if (rc != MKQ_OK) return rc;
   }
@@ -111,16 +121,30 @@ int gemv_typed(const void* xv, const void* wv, const void* rv, void* yv, int bat
 
 }  // namespace
 
+static int gemv_dispatch(int dtype, const void* x, const void* w, const void* residual, void* y, void* sum, int batch,
+                         int in_features, int out_features, hipStream_t s) {
+  switch (dtype) {
+    case MKQ_DTYPE_BF16: return gemv_typed<bf16_t>(x, w, residual, y, sum, batch, in_features, out_features, s);
+    case MKQ_DTYPE_F16: return gemv_typed<f16_t>(x, w, residual, y, sum, batch, in_features, out_features, s);
+    case MKQ_DTYPE_F32: return gemv_typed<float>(x, w, residual, y, sum, batch, in_features, out_features, s);
+    default: return set_error(MKQ_ERR_INVALID, "gemv: unknown dtype %d", dtype);
+  }
+}
+
 extern "C" int mkq_gemv(int dtype, const void* x, const void* w, const void* residual, void* y, int batch,
                         int in_features, int out_features, void* stream) {
   clear_error();
   MKQ_REQUIRE(batch > 0 && in_features > 0 && out_features > 0, "gemv: sizes must be positive");
   MKQ_REQUIRE(x && w && y, "gemv: null tensor pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case MKQ_DTYPE_BF16: return gemv_typed<bf16_t>(x, w, residual, y, batch, in_features, out_features, s);
-    case MKQ_DTYPE_F16: return gemv_typed<f16_t>(x, w, residual, y, batch, in_features, out_features, s);
-    case MKQ_DTYPE_F32: return gemv_typed<float>(x, w, residual, y, batch, in_features, out_features, s);
-    default: return set_error(MKQ_ERR_INVALID, "gemv: unknown dtype %d", dtype);
-  }
+  return gemv_dispatch(dtype, x, w, residual, y, nullptr, batch, in_features, out_features,
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mkq_gemv_add(int dtype, const void* x, const void* w, const void* residual, void* y, void* sum,
+                            int batch, int in_features, int out_features, void* stream) {
+  clear_error();
+  MKQ_REQUIRE(batch > 0 && in_features > 0 && out_features > 0, "gemv_add: sizes must be positive");
+  MKQ_REQUIRE(x && w && residual && y && sum, "gemv_add: null tensor pointer");
+  return gemv_dispatch(dtype, x, w, residual, y, sum, batch, in_features, out_features,
+                       static_cast<hipStream_t>(stream));
 }

@@ -361,6 +361,27 @@ torch::Tensor gemv(torch::Tensor x, torch::Tensor w, c10::optional<torch::Tensor
   return y;
 }
 
+std::tuple<torch::Tensor, torch::Tensor> gemv_add(torch::Tensor x, torch::Tensor w, torch::Tensor residual) {
+  MK_CHECK_INPUT(x);
+  MK_CHECK_INPUT(w);
+  MK_CHECK_INPUT(residual);
+  TORCH_CHECK(x.dim() == 2, "x must be [batch, in_features]");
+  TORCH_CHECK(w.dim() == 2, "w must be [out_features, in_features]");
+  TORCH_CHECK(w.size(1) == x.size(1), "in_features mismatch");
+  TORCH_CHECK(x.scalar_type() == w.scalar_type() && x.scalar_type() == residual.scalar_type(),
+              "x, w and residual dtype mismatch");
+  TORCH_CHECK(residual.dim() == 2 && residual.size(0) == x.size(0) && residual.size(1) == w.size(0),
+              "residual must be [batch, out_features]");
+  c10::DeviceGuard guard(x.device());
+  auto y = torch::empty({x.size(0), w.size(0)}, x.options());
+  auto sum = torch::empty_like(y);
+  const int rc = mkq_gemv_add(to_mkq_dtype(x), x.data_ptr(), w.data_ptr(), residual.data_ptr(), y.data_ptr(),
+                              sum.data_ptr(), static_cast<int>(x.size(0)), static_cast<int>(x.size(1)),
+                              static_cast<int>(w.size(0)), current_stream());
+  check_status(rc, "gemv_add");
+  return {y, sum};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -377,5 +398,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gated_delta_decode_", &gated_delta_decode_, "Gated delta rule decode, state updated in place (HIP)");
   m.def("gemv", &gemv, "y = x w^T (+ residual) (HIP)", pybind11::arg("x"), pybind11::arg("w"),
         pybind11::arg("residual") = pybind11::none());
+  m.def("gemv_add", &gemv_add, "(y, residual + y) with y = x w^T (HIP)", pybind11::arg("x"), pybind11::arg("w"),
+        pybind11::arg("residual"));
   m.def("abi_version", &mkq_abi_version);
 }

@@ -29,7 +29,7 @@ from __future__ import annotations
 import math
 import weakref
 from dataclasses import dataclass
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -361,11 +361,24 @@ def linear_attention_decode(inputs: LinearAttentionInputs) -> tuple[torch.Tensor
     )
 
 
-def _project(out: torch.Tensor, out_proj: Optional[torch.Tensor], hidden: torch.Tensor) -> torch.Tensor:
+def _project_add(
+    out: torch.Tensor, out_proj: Optional[torch.Tensor], hidden: torch.Tensor
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(y, hidden + y) for the mixer output y (reference ops.py:721-723,
+    727-729).  Without out_proj, y is the output reshaped onto the hidden size
+    as in the reference.  With it, y = out @ out_proj^T and the residual add
+    runs in the GEMV's epilogue: y is rounded first, then added, the same two
+    roundings as the separate add."""
     if out_proj is None:
-        return out.reshape_as(hidden)
+        y = out.reshape_as(hidden)
+        return y, hidden + y
     _require_extension("decode_layer out_proj", out, out_proj)
-    return _C.gemv(out.reshape(out.shape[0], -1).contiguous(), out_proj.contiguous(), None)
+    x2 = out.reshape(out.shape[0], -1).contiguous()
+    if hidden.dtype != out.dtype:
+        y = _C.gemv(x2, out_proj.contiguous(), None)
+        return y, hidden + y
+    y, summed = _C.gemv_add(x2, out_proj.contiguous(), hidden.reshape(x2.shape[0], -1).contiguous())
+    return y, summed.reshape_as(hidden)
 
 
 def decode_layer(
@@ -391,14 +404,12 @@ def decode_layer(
     if kind == "full_attention":
         if full_attention is None:
             raise ValueError("full_attention inputs are required for full_attention layers")
-        attention_output = _project(full_attention_decode(full_attention), full_attention.out_proj, hidden)
-        residual = residual + attention_output
+        attention_output, residual = _project_add(full_attention_decode(full_attention), full_attention.out_proj, hidden)
     elif kind == "linear_attention":
         if linear_attention is None:
             raise ValueError("linear_attention inputs are required for linear_attention layers")
         linear_output, linear_state = linear_attention_decode(linear_attention)
-        linear_output = _project(linear_output, linear_attention.out_proj, hidden)
-        residual = residual + linear_output
+        linear_output, residual = _project_add(linear_output, linear_attention.out_proj, hidden)
     else:
         raise ValueError(f"unsupported layer_type: {kind}")
 

@@ -18,6 +18,7 @@ import torch
 
 import mega_kernel_qwen36 as mk
 import oracle
+from mega_kernel_qwen36 import _lib
 from tests.inputs import (assert_close_out, assert_close_state, make_attention, make_dense, make_gated_delta,
                           make_moe, np32)
 
@@ -127,3 +128,50 @@ def test_decode_layer_graph_replay():
         assert torch.equal(res.linear_state, eager.linear_state)
         mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)  # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("batch,dtype", [(1, torch.bfloat16), (5, torch.bfloat16), (3, torch.float16),
+                                         (2, torch.float32)])
+def test_gemv_add_matches_separate_add(batch, dtype):
+    """mkq_gemv_add through the C ABI, the fused residual add of decode_layer:
+    y is bit-identical to mkq_gemv without a residual, sum is bit-identical to
+    the reference's separate add (torch's `residual + y`), and y agrees with an
+    FP64 product within the output tolerance.  Batch 5 takes two launches
+    (4 rows, then 1)."""
+    lib = _lib.load_library()
+    g = torch.Generator().manual_seed(300 + batch)
+    kdim, n = 4096, 2048
+    x = torch.randn(batch, kdim, generator=g).to("cuda", dtype)
+    w = (torch.randn(n, kdim, generator=g) * 0.02).to("cuda", dtype)
+    r = torch.randn(batch, n, generator=g).to("cuda", dtype)
+    y, summed, y0 = (torch.empty(batch, n, dtype=dtype, device="cuda") for _ in range(3))
+    code = {torch.bfloat16: _lib.MKQ_DTYPE_BF16, torch.float16: _lib.MKQ_DTYPE_F16,
+            torch.float32: _lib.MKQ_DTYPE_F32}[dtype]
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.mkq_gemv_add(code, x.data_ptr(), w.data_ptr(), r.data_ptr(), y.data_ptr(), summed.data_ptr(), batch,
+                          kdim, n, stream)
+    assert rc == _lib.MKQ_OK, lib.mkq_last_error()
+    rc = lib.mkq_gemv(code, x.data_ptr(), w.data_ptr(), None, y0.data_ptr(), batch, kdim, n, stream)
+    assert rc == _lib.MKQ_OK, lib.mkq_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0)
+    assert torch.equal(summed, r + y)
+    ref = x.cpu().double() @ w.cpu().double().T
+    torch.testing.assert_close(y.cpu().double(), ref, atol=1e-2, rtol=1e-2)
+
+
+def test_decode_layer_projected_residual_equals_separate_add():
+    """decode_layer with an out_proj fuses the residual add into the
+    projection; its hidden output equals the unfused composition (projection,
+    torch add, MoE) bit for bit."""
+    x, w, k = make_moe(batch=2, seed=151)
+    lin = make_gated_delta(batch=2, seed=152)
+    lin = dataclasses.replace(lin, out_proj=_proj(x.shape[1], 32 * 128, 153))
+    res = mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+    out, _ = mk.linear_attention_decode(lin)
+    y = mk.ops._C.gemv(out.reshape(2, -1).contiguous(), lin.out_proj, None)
+    hidden, idx, _ = mk.moe_decode(x + y, w, top_k=k, add_residual=True)
+    torch.cuda.synchronize()
+    assert torch.equal(res.linear_output, y)
+    assert torch.equal(res.router_indices, idx)
+    assert torch.equal(res.hidden, hidden)

@@ -86,6 +86,20 @@ def test_rope_entry_rejects_unsupported_rotary_dims_without_gpu():
     assert b"null cos/sin pointer" in lib.mkq_last_error()
 
 
+def test_gemv_add_rejects_null_pointers_without_gpu():
+    """mkq_gemv_add needs the residual and both outputs; the checks run on the
+    host before any launch, so host buffers are never touched."""
+    lib = _lib.load_library()
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.addressof(buf)
+    for args in ((p, p, None, p, p), (p, p, p, p, None), (p, p, p, None, p)):
+        rc = lib.mkq_gemv_add(_lib.MKQ_DTYPE_BF16, *args, 1, 8, 8, None)
+        assert rc == _lib.MKQ_ERR_INVALID
+        assert b"null tensor pointer" in lib.mkq_last_error()
+    rc = lib.mkq_gemv_add(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, 0, 8, 8, None)
+    assert rc == _lib.MKQ_ERR_INVALID
+
+
 def test_workspace_sizes():
     lib = _lib.load_library()
     # act [batch, intermediate] FP32 plus the batched path's fragments, partials and counters
