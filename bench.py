@@ -265,6 +265,29 @@ def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
                 out[name] = r
                 log(f"attention T={t} with RoPE ({'keys rotated in the kernel' if 'python' not in name else 'cache rotated in torch first'}): "
                     f"{r['median_us']:.2f} us cold in stream, {r['warm_median_us']:.2f} us warm")
+            # KV append into a preallocated cache (capacity T + 64): the new
+            # row written by the attention kernel, against writing it with
+            # torch and then attending over the first T tokens.
+            cap = t + 64
+            kc = torch.zeros(1, cap, 4, 256, dtype=inp.k_cache.dtype, device="cuda")
+            vc = torch.zeros_like(kc)
+            kc[:, :t] = inp.k_cache
+            vc[:, :t] = inp.v_cache
+            kn, vn = inp.k_cache[:, t - 1].clone(), inp.v_cache[:, t - 1].clone()
+            app = mk.FullAttentionInputs(q=inp.q, k_cache=kc, v_cache=vc, k_new=kn, v_new=vn, cache_seqlen=t - 1)
+
+            def write_then_attend():
+                kc[:, t - 1] = kn
+                vc[:, t - 1] = vn
+                return mk.full_attention_decode(mk.FullAttentionInputs(q=inp.q, k_cache=kc[:, :t], v_cache=vc[:, :t]))
+
+            for name, f in (("attn_append_t32768", lambda: mk.full_attention_decode(app)),
+                            ("attn_append_torch_t32768", write_then_attend)):
+                r = measure(timer, f, steps, warmup, attn_bytes(1, 24, 4, 256, t))
+                out[name] = r
+                log(f"attention T={t} with KV append ({'in the kernel' if 'torch' not in name else 'row written by torch first'}): "
+                    f"{r['median_us']:.2f} us cold in stream, {r['warm_median_us']:.2f} us warm")
+            del kc, vc
         del inp
         torch.cuda.empty_cache()
     return out

@@ -119,6 +119,27 @@ int mkq_full_attention_decode_rope(int dtype, const void* q, const void* k_cache
                                    int seq_len, float scale, const float* cos_sin, int rotary_dim,
                                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* KV append fused into the attention step.  The caches are [batch, capacity,
+ * kv_heads, head_dim]; tokens 0 .. seq_len-2 are already in them and the new
+ * token's k_new, v_new [batch, kv_heads, head_dim] go to row seq_len - 1 of
+ * every batch row (written in place).  The result is that of
+ * mkq_full_attention_decode(_rope) over the first seq_len tokens after the
+ * cache rows were written, bit for bit; the kernel uses k_new/v_new directly
+ * for the new token, so it is never read back.  capacity >= seq_len; the
+ * batch stride is capacity tokens, so a preallocated cache needs no copy.
+ * cos_sin may be NULL (no rotation) or as in the _rope entry point; the
+ * cache keeps the new key unrotated, as the reference's caches hold unrotated
+ * keys that every call rotates (ops.py:368).  bf16/f16, head_dim % 8 == 0 and
+ * 16-byte aligned tensors, else MKQ_ERR_UNSUPPORTED (nothing written).  The
+ * workspace is sized for seq_len.  No counterpart in the reference, whose
+ * callers write the cache themselves before full_attention_decode
+ * (ops.py:367-374). */
+int mkq_full_attention_decode_append(int dtype, const void* q, const void* k_new, const void* v_new,
+                                     void* k_cache, void* v_cache, void* out, int batch, int q_heads,
+                                     int kv_heads, int head_dim, int seq_len, int capacity, float scale,
+                                     const float* cos_sin, int rotary_dim, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Recurrent linear-attention decode, reference rule.  Replaces
  *   _C.linear_attention_decode    (csrc/bindings.cpp:35, csrc/linear_attention_decode.cu:46-93)

@@ -159,12 +159,21 @@ size_t chunk_lds_bytes(int d, int heads) {
 // the sum are rounded separately and the result is rounded to T, as the
 // reference's torch ops do, so the rotated q and keys are bit-identical to
 // the reference's.
-template <typename T, int DT, bool ROPE>
+//
+// APP (KV append): token seq - 1 is the new one.  Its key and value come from
+// k_new/v_new [B, Hkv, D] rather than the cache: the workgroups of the last
+// chunk load them with q, write them over the stale row of the staged tile
+// (before any rotation), and the first head group's wave 0 stores them into
+// the cache row (kw/vw, the cache pointers) at the end.  No workgroup of the
+// launch reads that cache row and uses it.  `cap` is the cache's token
+// capacity (batch stride in tokens); seq <= cap.
+template <typename T, int DT, bool ROPE, bool APP>
 __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, float* __restrict__ part_o,
     float* __restrict__ part_m, float* __restrict__ part_l, T* __restrict__ out, const float* __restrict__ rope_cs,
-    int rot, int rope_lds_off, int hq, int hkv, int d, int seq, int group, int ngroups, int units, int nch,
-    int chunk_tokens, float scale_log2) {
+    const T* __restrict__ k_new, const T* __restrict__ v_new, T* kw, T* vw, int cap, int rot, int rope_lds_off,
+    int hq, int hkv, int d, int seq, int group, int ngroups, int units, int nch, int chunk_tokens,
+    float scale_log2) {
   typedef typename Mfma<T>::vec8 V8;
   typedef typename Mfma<T>::vec4 V4;
   constexpr int NS = DT / 32;               // QK^T MFMA steps over head_dim
@@ -188,7 +197,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
 
   // Descriptors over this unit's K/V rows of the chunk; anything past the
   // last row (tail tokens, the prefetch after the last tile) reads zero.
-  const size_t base = (size_t(b) * seq + t_begin) * hkv * d + size_t(kvh) * d;
+  const size_t base = (size_t(b) * cap + t_begin) * hkv * d + size_t(kvh) * d;
   const uint32_t bytes = (uint32_t(len) - 1) * tsb + uint32_t(d) * sizeof(T);
   const rsrc_t kr = make_rsrc(kc + base, bytes);
   const rsrc_t vr = make_rsrc(vc + base, bytes);
@@ -217,6 +226,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const rsrc_t cr = make_rsrc(rope_cs, uint32_t(2 * rot) * 4u);
     cs_ld[0] = buf_loadf(cr, uint32_t(threadIdx.x) * 4u);
     cs_ld[1] = buf_loadf(cr, uint32_t(threadIdx.x + kThreads) * 4u);
+  }
+  // APP: lane l < D/8 of every wave of the last chunk holds dims 8l..8l+7 of
+  // the new key and value (other workgroups read nothing: an empty range).
+  const int arow = seq - 1 - t_begin;  // the new token's row in this chunk
+  const bool owner = APP && arow < len;
+  u32x4 kap = u32x4{0u, 0u, 0u, 0u}, vap = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (APP) {
+    const uint32_t nb = owner ? uint32_t(d * sizeof(T)) : 0u;
+    const uint32_t off = lane * 8 < d ? uint32_t(lane * 16) : kFar;
+    kap = buf_load16(make_rsrc(k_new + (size_t(b) * hkv + kvh) * d, nb), off);
+    vap = buf_load16(make_rsrc(v_new + (size_t(b) * hkv + kvh) * d, nb), off);
   }
   // K and V chunk i of a tile: token row qi / CPR, dims 8 * (qi % CPR),
   // qi = lane + 64 i (two 512-byte token rows per load at D = 256).
@@ -280,6 +300,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
       const int qi = lane + kWave * i;
       *reinterpret_cast<u32x4*>(stage + (qi / CPR) * KSTR + (qi % CPR) * 16) = kreg[i];
     }
+    // APP: the new token's key over its stale row (same wave, program order).
+    const int ar = arow - t0;
+    const bool arow_here = owner && ar >= 0 && ar < kTT;
+    if constexpr (APP) {
+      if (arow_here && lane * 8 < d) *reinterpret_cast<u32x4*>(stage + ar * KSTR + lane * 16) = kap;
+    }
     if constexpr (ROPE) {
       // Rotary chunks, k' = k cos + rotate_half(k) sin: the tile's 16 * rot/8
       // of them spread over the wave's lanes (chunk j = row j / nrc, chunk
@@ -336,6 +362,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
       uint2* dst = reinterpret_cast<uint2*>(vt + (qi / CPR) * VSTR + (qi % CPR) * 8);
       dst[0] = make_uint2(vreg[i].x, vreg[i].y);
       dst[1] = make_uint2(vreg[i].z, vreg[i].w);
+    }
+    if constexpr (APP) {
+      if (arow_here && lane * 8 < d) {
+        uint2* dst = reinterpret_cast<uint2*>(vt + ar * VSTR + lane * 8);
+        dst[0] = make_uint2(vap.x, vap.y);
+        dst[1] = make_uint2(vap.z, vap.w);
+      }
     }
     if (pf) {
 #pragma unroll
@@ -422,6 +455,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
         part_m[pi] = M;
         part_l[pi] = L;
       }
+    }
+  }
+  if constexpr (APP) {
+    if (owner && hg == 0 && wave == 0 && lane * 8 < d) {
+      const size_t row = (size_t(b) * cap + (seq - 1)) * hkv * d + size_t(kvh) * d + size_t(lane) * 8;
+      *reinterpret_cast<u32x4*>(kw + row) = kap;
+      *reinterpret_cast<u32x4*>(vw + row) = vap;
     }
   }
 }
@@ -594,9 +634,16 @@ int plan_chunks(int units, int hkv, int d, int seq, size_t elt, Chunking* out) {
 
 size_t fast_ws_floats(int batch, int hq, int d, int seq) { return size_t(batch) * hq * max_chunks(seq) * (size_t(d) + 2); }
 
+// Appending launches pass k_new/v_new (non-null) and the cache capacity.
+struct Append {
+  const void* k_new = nullptr;
+  const void* v_new = nullptr;
+  int cap = 0;
+};
+
 template <typename T, int DT>
 int launch_fast(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
-                float scale, const float* rope_cs, int rot, float* ws, hipStream_t stream) {
+                float scale, const float* rope_cs, int rot, const Append& ap, float* ws, hipStream_t stream) {
   const int group = hq / hkv;
   const int ngroups = (group + 15) / 16;
   const int units = batch * hkv * ngroups;
@@ -606,25 +653,33 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   const size_t lds = chunk_lds_bytes<DT>(d, group < 16 ? group : 16);
   static bool attr_set = false;
   if (!attr_set) {
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    int(chunk_lds_bytes<DT>(DT, 16))));
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    int(chunk_lds_bytes<DT>(DT, 16) + 16 + 2 * kMaxD * sizeof(float))));
+    const int plain = int(chunk_lds_bytes<DT>(DT, 16));
+    const int roped = int(chunk_lds_bytes<DT>(DT, 16) + 16 + 2 * kMaxD * sizeof(float));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, plain));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, roped));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, plain));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, roped));
     attr_set = true;
   }
   MKQ_REQUIRE(size_t(ch.nch) * units < (size_t(1) << 31), "full_attention_decode: grid too large");
   float* part_o = ws;
   float* part_m = part_o + size_t(batch) * hq * ch.nch * d;
   float* part_l = part_m + size_t(batch) * hq * ch.nch;
-  auto* kern = rot > 0 ? attn_chunk_kernel<T, DT, true> : attn_chunk_kernel<T, DT, false>;
+  const bool app = ap.k_new != nullptr;
+  auto* kern = rot > 0 ? (app ? attn_chunk_kernel<T, DT, true, true> : attn_chunk_kernel<T, DT, true, false>)
+                       : (app ? attn_chunk_kernel<T, DT, false, true> : attn_chunk_kernel<T, DT, false, false>);
   const size_t rope_off = (lds + 15) / 16 * 16;  // the cos/sin table follows the staging/merge area
   const size_t lds_all = rot > 0 ? rope_off + size_t(2 * rot) * sizeof(float) : lds;
   kern<<<dim3(ch.nch * units), kThreads, lds_all, stream>>>(
       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), part_o, part_m, part_l,
-      static_cast<T*>(out), rope_cs, rot, int(rope_off), hq, hkv, d, seq, group, ngroups, units, ch.nch,
-      ch.chunk_tokens, scale * kLog2e);
+      static_cast<T*>(out), rope_cs, static_cast<const T*>(ap.k_new), static_cast<const T*>(ap.v_new),
+      app ? static_cast<T*>(const_cast<void*>(k)) : nullptr, app ? static_cast<T*>(const_cast<void*>(v)) : nullptr,
+      app ? ap.cap : seq, rot, int(rope_off), hq, hkv, d, seq, group, ngroups, units, ch.nch, ch.chunk_tokens,
+      scale * kLog2e);
   MKQ_LAUNCH_CHECK("attn_chunk_kernel");
   if (ch.nch > 1) {
     dim3 g2(batch * hq, (d + kWave - 1) / kWave);
@@ -636,10 +691,11 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
 
 template <typename T>
 int launch_fast_d(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
-                  float scale, const float* rope_cs, int rot, float* ws, hipStream_t stream) {
-  if (d <= 64) return launch_fast<T, 64>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ws, stream);
-  if (d <= 128) return launch_fast<T, 128>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ws, stream);
-  return launch_fast<T, 256>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ws, stream);
+                  float scale, const float* rope_cs, int rot, const Append& ap, float* ws, hipStream_t stream) {
+  if (d <= 64) return launch_fast<T, 64>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, ws, stream);
+  if (d <= 128)
+    return launch_fast<T, 128>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, ws, stream);
+  return launch_fast<T, 256>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, ws, stream);
 }
 
 template <typename T>
@@ -668,7 +724,8 @@ namespace {
 
 int attention_entry(const char* fn, int dtype, const void* q, const void* k_cache, const void* v_cache, void* out,
                     int batch, int q_heads, int kv_heads, int head_dim, int seq_len, float scale,
-                    const float* rope_cs, int rot, void* workspace, size_t workspace_bytes, void* stream) {
+                    const float* rope_cs, int rot, const Append& ap, void* workspace, size_t workspace_bytes,
+                    void* stream) {
   clear_error();
   MKQ_REQUIRE(batch > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0, "%s: sizes must be positive", fn);
   MKQ_REQUIRE(seq_len > 0, "seq_len must be positive");
@@ -683,6 +740,14 @@ int attention_entry(const char* fn, int dtype, const void* q, const void* k_cach
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* ws = static_cast<float*>(workspace);
   const bool fast_ok = (head_dim % 8 == 0) && aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
+  if (ap.k_new) {
+    MKQ_REQUIRE(ap.v_new, "%s: null tensor pointer", fn);
+    MKQ_REQUIRE(ap.cap >= seq_len, "%s: capacity %d is below seq_len %d", fn, ap.cap, seq_len);
+    if (!fast_ok || !aligned16(ap.k_new) || !aligned16(ap.v_new) ||
+        (dtype != MKQ_DTYPE_BF16 && dtype != MKQ_DTYPE_F16))
+      return set_error(MKQ_ERR_UNSUPPORTED,
+                       "%s: the in-kernel append needs bf16/f16, head_dim %% 8 == 0 and 16-byte aligned tensors", fn);
+  }
   if (rot > 0) {
     MKQ_REQUIRE(rope_cs, "%s: null cos/sin pointer", fn);
     if (!fast_ok || (dtype != MKQ_DTYPE_BF16 && dtype != MKQ_DTYPE_F16) || rot < 16 || rot > head_dim ||
@@ -695,12 +760,12 @@ int attention_entry(const char* fn, int dtype, const void* q, const void* k_cach
   switch (dtype) {
     case MKQ_DTYPE_BF16:
       return fast_ok ? launch_fast_d<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                             scale, rope_cs, rot, ws, s)
+                                             scale, rope_cs, rot, ap, ws, s)
                      : launch_generic<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                               scale, ws, s);
     case MKQ_DTYPE_F16:
       return fast_ok ? launch_fast_d<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                            scale, rope_cs, rot, ws, s)
+                                            scale, rope_cs, rot, ap, ws, s)
                      : launch_generic<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                              scale, ws, s);
     case MKQ_DTYPE_F32:
@@ -717,7 +782,7 @@ extern "C" int mkq_full_attention_decode(int dtype, const void* q, const void* k
                                          void* out, int batch, int q_heads, int kv_heads, int head_dim, int seq_len,
                                          float scale, void* workspace, size_t workspace_bytes, void* stream) {
   return attention_entry("full_attention_decode", dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads,
-                         head_dim, seq_len, scale, nullptr, 0, workspace, workspace_bytes, stream);
+                         head_dim, seq_len, scale, nullptr, 0, Append{}, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mkq_full_attention_decode_rope(int dtype, const void* q, const void* k_cache, const void* v_cache,
@@ -725,5 +790,24 @@ extern "C" int mkq_full_attention_decode_rope(int dtype, const void* q, const vo
                                               int seq_len, float scale, const float* cos_sin, int rotary_dim,
                                               void* workspace, size_t workspace_bytes, void* stream) {
   return attention_entry("full_attention_decode_rope", dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads,
-                         head_dim, seq_len, scale, cos_sin, rotary_dim, workspace, workspace_bytes, stream);
+                         head_dim, seq_len, scale, cos_sin, rotary_dim, Append{}, workspace, workspace_bytes,
+                         stream);
+}
+
+extern "C" int mkq_full_attention_decode_append(int dtype, const void* q, const void* k_new, const void* v_new,
+                                                void* k_cache, void* v_cache, void* out, int batch, int q_heads,
+                                                int kv_heads, int head_dim, int seq_len, int capacity, float scale,
+                                                const float* cos_sin, int rotary_dim, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+  const char* fn = "full_attention_decode_append";
+  if (!k_new || !v_new) {
+    clear_error();
+    return set_error(MKQ_ERR_INVALID, "%s: null tensor pointer", fn);
+  }
+  Append ap;
+  ap.k_new = k_new;
+  ap.v_new = v_new;
+  ap.cap = capacity;
+  return attention_entry(fn, dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
+                         cos_sin, cos_sin ? rotary_dim : 0, ap, workspace, workspace_bytes, stream);
 }

@@ -250,6 +250,54 @@ torch::Tensor full_attention_decode_rope(torch::Tensor q, torch::Tensor k_cache,
   return attention_impl(q, k_cache, v_cache, scale, &cos_sin, rotary_dim);
 }
 
+// Writes k_new/v_new [batch, kv_heads, head_dim] into row seq_len - 1 of the
+// caches [batch, capacity, kv_heads, head_dim] (in place) and attends over
+// the first seq_len tokens; cos_sin as for full_attention_decode_rope or None.
+torch::Tensor full_attention_decode_append(torch::Tensor q, torch::Tensor k_new, torch::Tensor v_new,
+                                           torch::Tensor k_cache, torch::Tensor v_cache, int64_t seq_len, double scale,
+                                           c10::optional<torch::Tensor> cos_sin, int64_t rotary_dim) {
+  MK_CHECK_INPUT(q);
+  MK_CHECK_INPUT(k_new);
+  MK_CHECK_INPUT(v_new);
+  MK_CHECK_INPUT(k_cache);
+  MK_CHECK_INPUT(v_cache);
+  TORCH_CHECK(q.dim() == 3, "q must be [batch, query_heads, head_dim]");
+  TORCH_CHECK(k_cache.dim() == 4, "k_cache must be [batch, capacity, kv_heads, head_dim]");
+  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "v_cache shape must match k_cache");
+  TORCH_CHECK(q.scalar_type() == k_cache.scalar_type() && q.scalar_type() == v_cache.scalar_type() &&
+                  q.scalar_type() == k_new.scalar_type() && q.scalar_type() == v_new.scalar_type(),
+              "q, k_new, v_new and the caches must share a dtype");
+  const int batch = static_cast<int>(q.size(0));
+  const int query_heads = static_cast<int>(q.size(1));
+  const int head_dim = static_cast<int>(q.size(2));
+  const int capacity = static_cast<int>(k_cache.size(1));
+  const int kv_heads = static_cast<int>(k_cache.size(2));
+  TORCH_CHECK(k_cache.size(0) == batch && k_cache.size(3) == head_dim, "k_cache batch/head_dim mismatch");
+  TORCH_CHECK(k_new.dim() == 3 && k_new.size(0) == batch && k_new.size(1) == kv_heads && k_new.size(2) == head_dim,
+              "k_new must be [batch, kv_heads, head_dim]");
+  TORCH_CHECK(v_new.sizes() == k_new.sizes(), "v_new shape must match k_new");
+  TORCH_CHECK(kv_heads > 0 && query_heads % kv_heads == 0, "query_heads must be divisible by kv_heads");
+  TORCH_CHECK(seq_len > 0 && seq_len <= capacity, "seq_len must be in [1, capacity]");
+  const float* cs = nullptr;
+  if (cos_sin.has_value()) {
+    TORCH_CHECK(cos_sin->is_cuda() && cos_sin->is_contiguous() && cos_sin->scalar_type() == torch::kFloat32,
+                "cos_sin must be a contiguous float32 device tensor");
+    TORCH_CHECK(cos_sin->numel() == 2 * rotary_dim, "cos_sin must hold 2 * rotary_dim values");
+    cs = cos_sin->data_ptr<float>();
+  }
+  c10::DeviceGuard guard(q.device());
+  auto out = torch::empty_like(q);
+  const int seq = static_cast<int>(seq_len);
+  auto ws = workspace_for(Ws::kAttention, q,
+                          mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq));
+  const int rc = mkq_full_attention_decode_append(
+      to_mkq_dtype(q), q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+      out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq, capacity, static_cast<float>(scale), cs,
+      static_cast<int>(rotary_dim), ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream());
+  check_status(rc, "full_attention_decode_append");
+  return out;
+}
+
 std::tuple<torch::Tensor, torch::Tensor> linear_attention_decode(torch::Tensor q, torch::Tensor k, torch::Tensor v,
                                                                  torch::Tensor state, double decay) {
   // Checks and messages as in linear_attention_decode.cu:52-69.
@@ -393,6 +441,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("full_attention_decode", &full_attention_decode, "Split-K GQA flash-decode (HIP)");
   m.def("full_attention_decode_rope", &full_attention_decode_rope,
         "Split-K GQA flash-decode with the keys rotated on the fly (HIP)");
+  m.def("full_attention_decode_append", &full_attention_decode_append,
+        "KV append fused into the split-K GQA flash-decode (HIP)", pybind11::arg("q"), pybind11::arg("k_new"),
+        pybind11::arg("v_new"), pybind11::arg("k_cache"), pybind11::arg("v_cache"), pybind11::arg("seq_len"),
+        pybind11::arg("scale"), pybind11::arg("cos_sin") = pybind11::none(), pybind11::arg("rotary_dim") = 0);
   m.def("linear_attention_decode", &linear_attention_decode, "Recurrent linear-attention decode (HIP)");
   m.def("gated_delta_decode", &gated_delta_decode, "Gated delta rule decode (HIP)");
   m.def("gated_delta_decode_", &gated_delta_decode_, "Gated delta rule decode, state updated in place (HIP)");

@@ -26,6 +26,7 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
+import dataclasses
 import math
 import weakref
 from dataclasses import dataclass
@@ -89,6 +90,13 @@ class FullAttentionInputs:
     rotary_dim: int = 64
     scale: Optional[float] = None
     out_proj: Optional[torch.Tensor] = None  # [hidden, q_heads*head_dim], used by decode_layer
+    # KV append (no counterpart in the reference): the new token's key and
+    # value [batch, kv_heads, head_dim], written in place into the caches'
+    # row `cache_seqlen` (default: their last row) before attending over the
+    # first cache_seqlen + 1 tokens.
+    k_new: Optional[torch.Tensor] = None
+    v_new: Optional[torch.Tensor] = None
+    cache_seqlen: Optional[int] = None
 
 
 @dataclass(frozen=True)
@@ -307,6 +315,49 @@ def _rope_in_kernel(inputs: FullAttentionInputs) -> Optional[torch.Tensor]:
     return cs
 
 
+def _attention_append(inputs: FullAttentionInputs) -> torch.Tensor:
+    """KV append fused into the attention step.  k_new/v_new go to row
+    p = cache_seqlen (default: the last row) of k_cache/v_cache [batch,
+    capacity, kv_heads, head_dim], in place, and the result is
+    full_attention_decode over the first p + 1 tokens.  Where the kernel
+    supports it (bf16/f16, head_dim % 8 == 0, 16-byte aligned tensors, RoPE in
+    the kernel or none), the attention kernel writes the rows itself and
+    uses the new key and value without reading them back; otherwise the rows
+    are written first.  The reference's callers write the cache themselves
+    before full_attention_decode (ops.py:367-374)."""
+    if inputs.k_new is None or inputs.v_new is None:
+        raise ValueError("k_new and v_new must be given together")
+    k_cache, v_cache = inputs.k_cache, inputs.v_cache
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache and v_cache must be [batch, capacity, kv_heads, head_dim]")
+    b, cap, hkv, d = k_cache.shape
+    pos = cap - 1 if inputs.cache_seqlen is None else int(inputs.cache_seqlen)
+    if not 0 <= pos < cap:
+        raise ValueError("cache_seqlen must leave room for the new token")
+    q = inputs.q
+    if q.shape[1] % hkv != 0:
+        raise ValueError("query_heads must be divisible by kv_heads")
+    k_new = inputs.k_new.reshape(b, hkv, d)
+    v_new = inputs.v_new.reshape(b, hkv, d)
+    _require_extension("full_attention_decode", q, k_cache, v_cache, k_new, v_new)
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache and v_cache must be contiguous: the new token is written in place")
+    rope = inputs.cos is not None and inputs.sin is not None
+    cs = _rope_in_kernel(inputs) if rope else None
+    if (k_cache.dtype in (torch.bfloat16, torch.float16) and d % 8 == 0 and (cs is not None or not rope)
+            and all(t.dtype == k_cache.dtype for t in (q, k_new, v_new, v_cache))):
+        qc, kn, vn = q.contiguous(), k_new.contiguous(), v_new.contiguous()
+        if all(t.data_ptr() % 16 == 0 for t in (qc, kn, vn, k_cache, v_cache)):
+            scale = inputs.scale if inputs.scale is not None else 1.0 / math.sqrt(d)
+            rot = int(inputs.rotary_dim) if cs is not None else 0
+            return _C.full_attention_decode_append(qc, kn, vn, k_cache, v_cache, pos + 1, float(scale), cs, rot)
+    k_cache[:, pos] = k_new
+    v_cache[:, pos] = v_new
+    return full_attention_decode(dataclasses.replace(inputs, k_cache=k_cache[:, :pos + 1],
+                                                     v_cache=v_cache[:, :pos + 1], k_new=None, v_new=None,
+                                                     cache_seqlen=None))
+
+
 def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:
     """One-token GQA attention over a contiguous KV cache (split-K flash-decode, HIP).
 
@@ -314,7 +365,10 @@ def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:
     kernel (ops.py:368).  Here, where the kernel supports it, q and the keys
     are rotated inside the kernel as the keys stream, with the same rounding;
     otherwise both are rotated first, as the reference does.  Device-resident
-    cos/sin avoid a host-to-device copy per call."""
+    cos/sin avoid a host-to-device copy per call.  With k_new/v_new the new
+    token is appended to the caches first (see _attention_append)."""
+    if inputs.k_new is not None or inputs.v_new is not None:
+        return _attention_append(inputs)
     cs = _rope_in_kernel(inputs)
     if cs is not None:
         q, k_cache = inputs.q, inputs.k_cache  # both rotated inside the kernel

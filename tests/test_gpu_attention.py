@@ -224,3 +224,105 @@ def test_attention_rope_cos_changed_in_place():
     plain = mk.full_attention_decode(mk.FullAttentionInputs(q=qr, k_cache=kr, v_cache=inp.v_cache))
     assert torch.equal(second, plain)
     assert not torch.equal(first, second)
+
+
+def _append_case(b, hq, hkv, d, cap, dtype, seed):
+    """q, the new token's k/v and caches of `cap` rows filled with stale values
+    everywhere (including the row the new token goes to)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, hq, d, generator=g).to("cuda", dtype)
+    k_new = torch.randn(b, hkv, d, generator=g).to("cuda", dtype)
+    v_new = torch.randn(b, hkv, d, generator=g).to("cuda", dtype)
+    k_cache = torch.randn(b, cap, hkv, d, generator=g).to("cuda", dtype)
+    v_cache = torch.randn(b, cap, hkv, d, generator=g).to("cuda", dtype)
+    return q, k_new, v_new, k_cache, v_cache
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,seq,cap,dtype,rot", [
+    (1, 24, 4, 256, 32768, 32768, torch.bfloat16, 0),   # config 4, the cache's last row
+    (1, 24, 4, 256, 32768, 33000, torch.bfloat16, 64),  # preallocated cache, RoPE in the kernel
+    (2, 8, 2, 128, 3001, 4096, torch.float16, 0),       # batch stride = capacity, not seq_len
+    (1, 32, 1, 64, 1, 16, torch.bfloat16, 32),          # the new token alone; two head groups
+    (3, 40, 2, 128, 700, 1024, torch.bfloat16, 0),      # group 20: two head groups share the row
+    (2, 16, 4, 256, 4097, 5000, torch.float16, 128),    # new token first in its tile
+])
+def test_attention_append_in_kernel_equals_written_cache(b, hq, hkv, d, seq, cap, dtype, rot):
+    """KV append inside the attention kernel: the output is bit-identical to
+    writing the new row with torch first and attending over the first seq_len
+    tokens with the plain (or RoPE) path, and afterwards the caches equal the
+    torch-written ones everywhere (the new row written, every other row
+    untouched)."""
+    q, k_new, v_new, k_cache, v_cache = _append_case(b, hq, hkv, d, cap, dtype, 400 + seq)
+    cos = sin = None
+    if rot:
+        ang = torch.rand(rot, generator=torch.Generator().manual_seed(seq)) * 6.0
+        cos, sin = torch.cos(ang)[None], torch.sin(ang)[None]
+    k_ref, v_ref = k_cache.clone(), v_cache.clone()
+    k_ref[:, seq - 1] = k_new
+    v_ref[:, seq - 1] = v_new
+    want = mk.full_attention_decode(mk.FullAttentionInputs(
+        q, k_ref[:, :seq].contiguous(), v_ref[:, :seq].contiguous(), cos=cos, sin=sin, rotary_dim=rot or 64))
+    got = mk.full_attention_decode(mk.FullAttentionInputs(
+        q, k_cache, v_cache, cos=cos, sin=sin, rotary_dim=rot or 64, k_new=k_new, v_new=v_new,
+        cache_seqlen=seq - 1))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(k_cache, k_ref)
+    assert torch.equal(v_cache, v_ref)
+    if rot == 0 and seq <= 4096:
+        inp = mk.FullAttentionInputs(q, k_ref[:, :seq].contiguous(), v_ref[:, :seq].contiguous(),
+                                     scale=1.0 / math.sqrt(d))
+        assert_close_out(got, _ref(inp))
+
+
+def test_attention_append_through_c_abi_then_next_step():
+    """Two decode steps through mkq_full_attention_decode_append on one
+    preallocated cache: each step's output matches the oracle on the cache as
+    written so far, and the second step reads the row the first one wrote."""
+    lib = _lib.load_library()
+    b, hq, hkv, d, cap, t0 = 1, 12, 2, 128, 2048, 1500
+    q, k_new, v_new, k_cache, v_cache = _append_case(b, hq, hkv, d, cap, torch.bfloat16, 77)
+    nbytes = lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t0 + 2)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for step in range(2):
+        seq = t0 + 1 + step
+        kn = k_new * (step + 1)
+        vn = v_new - step
+        expect_k, expect_v = k_cache.clone(), v_cache.clone()
+        expect_k[:, seq - 1] = kn
+        expect_v[:, seq - 1] = vn
+        out = torch.empty_like(q)
+        rc = lib.mkq_full_attention_decode_append(_lib.MKQ_DTYPE_BF16, q.data_ptr(), kn.data_ptr(), vn.data_ptr(),
+                                                  k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), b, hq, hkv,
+                                                  d, seq, cap, 1.0 / math.sqrt(d), None, 0, ws.data_ptr(), nbytes,
+                                                  stream)
+        assert rc == _lib.MKQ_OK, lib.mkq_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(k_cache, expect_k) and torch.equal(v_cache, expect_v)
+        inp = mk.FullAttentionInputs(q, k_cache[:, :seq].contiguous(), v_cache[:, :seq].contiguous(),
+                                     scale=1.0 / math.sqrt(d))
+        assert_close_out(out, _ref(inp))
+
+
+@pytest.mark.parametrize("d,dtype,rot", [(20, torch.bfloat16, 0), (64, torch.float32, 0), (128, torch.bfloat16, 24)])
+def test_attention_append_fallback_writes_then_attends(d, dtype, rot):
+    """Shapes the kernel cannot append in place (generic head_dim, FP32, a
+    rotary_dim it cannot rotate) write the rows with torch and take the other
+    paths; the result and the caches are the same as doing that by hand."""
+    b, hq, hkv, seq, cap = 2, 8, 2, 90, 128
+    q, k_new, v_new, k_cache, v_cache = _append_case(b, hq, hkv, d, cap, dtype, 500 + d)
+    cos = sin = None
+    if rot:
+        ang = torch.rand(rot, generator=torch.Generator().manual_seed(5)) * 6.0
+        cos, sin = torch.cos(ang)[None], torch.sin(ang)[None]
+    k_ref, v_ref = k_cache.clone(), v_cache.clone()
+    k_ref[:, seq - 1] = k_new
+    v_ref[:, seq - 1] = v_new
+    want = mk.full_attention_decode(mk.FullAttentionInputs(
+        q, k_ref[:, :seq].contiguous(), v_ref[:, :seq].contiguous(), cos=cos, sin=sin, rotary_dim=rot or 64))
+    got = mk.full_attention_decode(mk.FullAttentionInputs(
+        q, k_cache, v_cache, cos=cos, sin=sin, rotary_dim=rot or 64, k_new=k_new, v_new=v_new, cache_seqlen=seq - 1))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(k_cache, k_ref) and torch.equal(v_cache, v_ref)

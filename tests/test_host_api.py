@@ -86,6 +86,43 @@ def test_rope_entry_rejects_unsupported_rotary_dims_without_gpu():
     assert b"null cos/sin pointer" in lib.mkq_last_error()
 
 
+def test_append_entry_validates_on_the_host_without_gpu():
+    """mkq_full_attention_decode_append rejects what it cannot do before any
+    launch: a missing k_new/v_new or a capacity below seq_len (INVALID), and
+    FP32 or a head_dim that is not a multiple of 8 (UNSUPPORTED, nothing
+    written).  The buffers are host memory and are never touched."""
+    lib = _lib.load_library()
+    b, hq, hkv, d, t, cap = 1, 4, 2, 64, 8, 16
+    nbytes = lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t)
+    raw = ctypes.create_string_buffer(nbytes + 512)
+    ws = (ctypes.addressof(raw) + 255) // 256 * 256
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    call = lib.mkq_full_attention_decode_append
+    assert call(_lib.MKQ_DTYPE_BF16, p, None, p, p, p, p, b, hq, hkv, d, t, cap, 1.0, None, 0, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, p, b, hq, hkv, d, t, t - 1, 1.0, None, 0, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert b"capacity" in lib.mkq_last_error()
+    assert call(_lib.MKQ_DTYPE_F32, p, p, p, p, p, p, b, hq, hkv, d, t, cap, 1.0, None, 0, ws, nbytes,
+                None) == _lib.MKQ_ERR_UNSUPPORTED
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, p, b, hq, hkv, 20, t, cap, 1.0, None, 0, ws, nbytes,
+                None) == _lib.MKQ_ERR_UNSUPPORTED
+    assert b"append" in lib.mkq_last_error()
+
+
+def test_append_inputs_validated_before_any_device_work():
+    """The Python KV append checks its arguments first: both of k_new/v_new,
+    and a cache_seqlen that leaves a row for the new token."""
+    q = torch.zeros(1, 4, 64)
+    kc = torch.zeros(1, 8, 2, 64)
+    kn = torch.zeros(1, 2, 64)
+    with pytest.raises(ValueError, match="together"):
+        mk.full_attention_decode(mk.FullAttentionInputs(q, kc, kc.clone(), k_new=kn))
+    with pytest.raises(ValueError, match="room"):
+        mk.full_attention_decode(mk.FullAttentionInputs(q, kc, kc.clone(), k_new=kn, v_new=kn, cache_seqlen=8))
+
+
 def test_gemv_add_rejects_null_pointers_without_gpu():
     """mkq_gemv_add needs the residual and both outputs; the checks run on the
     host before any launch, so host buffers are never touched."""
