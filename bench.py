@@ -294,6 +294,8 @@ def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
 
 
 def bench_linear(mk, inputs, timer, steps, warmup, batches):
+    import dataclasses
+
     out = {}
     for b in batches:
         inp = inputs.make_gated_delta(batch=b)
@@ -302,6 +304,13 @@ def bench_linear(mk, inputs, timer, steps, warmup, batches):
         out[f"linear_b{b}"] = cold
         log(f"linear b={b}: {cold['median_us']:.2f} us cold in stream ({cold['gbps']:.0f} GB/s), "
             f"{cold['warm_median_us']:.2f} us warm, {cold['isolated_event_median_us']:.2f} us isolated launch")
+        # The same step with q/k L2-normalised and q scaled inside the kernel.
+        normed = dataclasses.replace(inp, qk_l2norm=True)
+        r = measure(timer, lambda: mk.linear_attention_decode(normed), steps, warmup,  # noqa: B023
+                    linear_bytes(b, 16, 32, 128, 128))
+        out[f"linear_qknorm_b{b}"] = r
+        log(f"linear b={b} with q/k L2 norm in the kernel: {r['median_us']:.2f} us cold in stream, "
+            f"{r['warm_median_us']:.2f} us warm")
     return out
 
 

@@ -165,6 +165,16 @@ int mkq_gated_delta_decode(int dtype, const void* q, const void* k, const void* 
                            float* new_state, int batch, int k_heads, int v_heads, int key_dim,
                            int value_dim, void* stream);
 
+/* The same step with q and k L2-normalised inside the kernel, in FP32,
+ * x / sqrt(sum x^2 + 1e-6) over key_dim, and q then multiplied by q_scale
+ * (1/sqrt(key_dim) in Qwen3.6): the use_qk_l2norm_in_kernel form of the
+ * model's linear-attention step, where otherwise the caller normalises q
+ * and k with separate ops first.  No counterpart in the reference. */
+int mkq_gated_delta_decode_qknorm(int dtype, const void* q, const void* k, const void* v,
+                                  const float* state, const float* g, const float* beta, void* out,
+                                  float* new_state, int batch, int k_heads, int v_heads, int key_dim,
+                                  int value_dim, float q_scale, void* stream);
+
 /* ------------------------------------------------------------------------
  * Plain GEMV used for the optional attention output projections in
  * decode_layer: y[b, n] = sum_k w[n, k] * x[b, k] (+ residual[b, n]).

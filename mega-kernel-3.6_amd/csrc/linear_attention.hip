@@ -12,6 +12,10 @@
 // waves split the key rows, and the two reductions over key rows (S^T k and
 // S'^T q) cross the waves through LDS.  The slice stays in VGPRs between the
 // single HBM read and the single HBM write of the state.
+//
+// With qk_norm, q and k are L2-normalised in FP32 as they are staged,
+// x / sqrt(sum x^2 + 1e-6), and q is then multiplied by q_scale: the
+// use_qk_l2norm_in_kernel form of the Qwen3.6 linear-attention step.
 #include "mkq_host.h"
 
 using namespace mkq;
@@ -28,10 +32,12 @@ template <typename T, bool GATED>
 __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* state,
     const float* __restrict__ g, const float* __restrict__ beta, T* __restrict__ out, float* new_state, int hk,
-    int hv, int dk, int dv, float decay) {
+    int hv, int dk, int dv, float decay, int qk_norm, float q_scale) {
+  static_assert(kMaxKeyDim == kThreads, "one staged q/k element per thread");
   __shared__ float qs[kMaxKeyDim];
   __shared__ float ks[kMaxKeyDim];
   __shared__ float red[kWaves][kWave];
+  __shared__ float nrm[kWaves][2];
 
   const int lane = threadIdx.x % kWave, wave = wave_id();
   const int j = blockIdx.x * kWave + lane;  // value column
@@ -41,31 +47,59 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
   const int qh = vh / rep;
   const bool col_ok = j < dv;
 
-  for (int i = threadIdx.x; i < kMaxKeyDim; i += kThreads) {  // zero past dk
-    qs[i] = i < dk ? to_f(q[(size_t(b) * hk + qh) * dk + i]) : 0.f;
-    ks[i] = i < dk ? to_f(k[(size_t(b) * hk + qh) * dk + i]) : 0.f;
-  }
-  float d = decay, bt = 1.0f;
-  if constexpr (GATED) {
-    d = expf(g[size_t(b) * hv + vh]);
-    bt = beta[size_t(b) * hv + vh];
-  }
-  const float vj = col_ok ? to_f(v[(size_t(b) * hv + vh) * dv + j]) : 0.f;
-  __syncthreads();
-
   // One descriptor over this head's state: rows i >= dk fall past its end and
   // read as zero, so all loads issue back to back with no branches.  Lanes
   // past the last column use an out-of-range offset.
   const size_t base = (size_t(b) * hv + vh) * size_t(dk) * dv;
   const rsrc_t srd = make_rsrc(state + base, uint32_t(size_t(dk) * dv * 4));
   const rsrc_t swr = make_rsrc(new_state + base, uint32_t(size_t(dk) * dv * 4));
+
+  // q, k and v first (unconditional loads at clamped indices, zeroed after,
+  // so no branch waits on them), then the state slice: the state loads are
+  // in flight while q/k are staged (and normalised).
+  const int ti = threadIdx.x;  // staged q/k element, zero past dk
+  const bool kin = ti < dk;
+  const size_t qo = (size_t(b) * hk + qh) * dk + (kin ? ti : 0);
+  float qv = to_f(q[qo]);
+  float kv = to_f(k[qo]);
+  const float vraw = to_f(v[(size_t(b) * hv + vh) * dv + (col_ok ? j : 0)]);
+  float d = decay, bt = 1.0f;
+  if constexpr (GATED) {
+    d = expf(g[size_t(b) * hv + vh]);
+    bt = beta[size_t(b) * hv + vh];
+  }
   float s[kRowsPerWave];
 #pragma unroll
   for (int r = 0; r < kRowsPerWave; ++r) {
     const int i = wave + r * kWaves;
     const uint32_t off = col_ok ? uint32_t((i * dv + j) * 4) : 0xFFFFFFF0u;
-    s[r] = buf_loadf(srd, off) * d;
+    s[r] = buf_loadf(srd, off);
   }
+
+  qv = kin ? qv : 0.f;
+  kv = kin ? kv : 0.f;
+  const float vj = col_ok ? vraw : 0.f;
+  if (qk_norm) {  // uniform over the launch
+    const float sq = wave_sum(qv * qv), sk = wave_sum(kv * kv);
+    if (lane == 0) {
+      nrm[wave][0] = sq;
+      nrm[wave][1] = sk;
+    }
+    __syncthreads();
+    float tq = 0.f, tk = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      tq += nrm[w][0];
+      tk += nrm[w][1];
+    }
+    qv = qv / sqrtf(tq + 1e-6f) * q_scale;
+    kv = kv / sqrtf(tk + 1e-6f);
+  }
+  qs[ti] = qv;
+  ks[ti] = kv;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kRowsPerWave; ++r) s[r] *= d;
 
   float add = vj;  // reference rule: S += k (x) v
   if constexpr (GATED) {
@@ -106,11 +140,12 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
 
 template <typename T, bool GATED>
 int launch(const void* q, const void* k, const void* v, const float* state, const float* g, const float* beta,
-           void* out, float* new_state, int batch, int hk, int hv, int dk, int dv, float decay, hipStream_t stream) {
+           void* out, float* new_state, int batch, int hk, int hv, int dk, int dv, float decay, int qk_norm,
+           float q_scale, hipStream_t stream) {
   dim3 grid((dv + kWave - 1) / kWave, hv, batch);
   linear_attention_kernel<T, GATED><<<grid, kThreads, 0, stream>>>(
       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), state, g, beta,
-      static_cast<T*>(out), new_state, hk, hv, dk, dv, decay);
+      static_cast<T*>(out), new_state, hk, hv, dk, dv, decay, qk_norm, q_scale);
   MKQ_LAUNCH_CHECK("linear_attention_kernel");
   return MKQ_OK;
 }
@@ -118,15 +153,18 @@ int launch(const void* q, const void* k, const void* v, const float* state, cons
 template <bool GATED>
 int dispatch(int dtype, const void* q, const void* k, const void* v, const float* state, const float* g,
              const float* beta, void* out, float* new_state, int batch, int hk, int hv, int dk, int dv, float decay,
-             void* stream) {
+             int qk_norm, float q_scale, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case MKQ_DTYPE_BF16:
-      return launch<bf16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, s);
+      return launch<bf16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, qk_norm,
+                                   q_scale, s);
     case MKQ_DTYPE_F16:
-      return launch<f16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, s);
+      return launch<f16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, qk_norm,
+                                  q_scale, s);
     case MKQ_DTYPE_F32:
-      return launch<float, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, s);
+      return launch<float, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, qk_norm,
+                                  q_scale, s);
     default:
       return set_error(MKQ_ERR_INVALID, "linear attention: unknown dtype %d", dtype);
   }
@@ -144,20 +182,38 @@ extern "C" int mkq_linear_attention_decode(int dtype, const void* q, const void*
     return set_error(MKQ_ERR_UNSUPPORTED, "linear_attention_decode: key_dim %d > %d", key_dim, kMaxKeyDim);
   MKQ_REQUIRE(batch <= 65535 && heads <= 65535, "linear_attention_decode: batch/heads too large");
   return dispatch<false>(dtype, q, k, v, state, nullptr, nullptr, out, new_state, batch, heads, heads, key_dim,
-                         value_dim, decay, stream);
+                         value_dim, decay, 0, 1.0f, stream);
 }
+
+namespace {
+
+int gated_entry(const char* fn, int dtype, const void* q, const void* k, const void* v, const float* state,
+                const float* g, const float* beta, void* out, float* new_state, int batch, int k_heads, int v_heads,
+                int key_dim, int value_dim, int qk_norm, float q_scale, void* stream) {
+  clear_error();
+  MKQ_REQUIRE(batch > 0 && k_heads > 0 && v_heads > 0 && key_dim > 0 && value_dim > 0, "%s: sizes must be positive",
+              fn);
+  MKQ_REQUIRE(v_heads % k_heads == 0, "%s: v_heads must be a multiple of k_heads", fn);
+  MKQ_REQUIRE(q && k && v && state && g && beta && out && new_state, "%s: null tensor pointer", fn);
+  if (key_dim > kMaxKeyDim) return set_error(MKQ_ERR_UNSUPPORTED, "%s: key_dim %d > %d", fn, key_dim, kMaxKeyDim);
+  MKQ_REQUIRE(batch <= 65535 && v_heads <= 65535, "%s: batch/heads too large", fn);
+  return dispatch<true>(dtype, q, k, v, state, g, beta, out, new_state, batch, k_heads, v_heads, key_dim, value_dim,
+                        1.0f, qk_norm, q_scale, stream);
+}
+
+}  // namespace
 
 extern "C" int mkq_gated_delta_decode(int dtype, const void* q, const void* k, const void* v, const float* state,
                                       const float* g, const float* beta, void* out, float* new_state, int batch,
                                       int k_heads, int v_heads, int key_dim, int value_dim, void* stream) {
-  clear_error();
-  MKQ_REQUIRE(batch > 0 && k_heads > 0 && v_heads > 0 && key_dim > 0 && value_dim > 0,
-              "gated_delta_decode: sizes must be positive");
-  MKQ_REQUIRE(v_heads % k_heads == 0, "gated_delta_decode: v_heads must be a multiple of k_heads");
-  MKQ_REQUIRE(q && k && v && state && g && beta && out && new_state, "gated_delta_decode: null tensor pointer");
-  if (key_dim > kMaxKeyDim)
-    return set_error(MKQ_ERR_UNSUPPORTED, "gated_delta_decode: key_dim %d > %d", key_dim, kMaxKeyDim);
-  MKQ_REQUIRE(batch <= 65535 && v_heads <= 65535, "gated_delta_decode: batch/heads too large");
-  return dispatch<true>(dtype, q, k, v, state, g, beta, out, new_state, batch, k_heads, v_heads, key_dim, value_dim,
-                        1.0f, stream);
+  return gated_entry("gated_delta_decode", dtype, q, k, v, state, g, beta, out, new_state, batch, k_heads, v_heads,
+                     key_dim, value_dim, 0, 1.0f, stream);
+}
+
+extern "C" int mkq_gated_delta_decode_qknorm(int dtype, const void* q, const void* k, const void* v,
+                                             const float* state, const float* g, const float* beta, void* out,
+                                             float* new_state, int batch, int k_heads, int v_heads, int key_dim,
+                                             int value_dim, float q_scale, void* stream) {
+  return gated_entry("gated_delta_decode_qknorm", dtype, q, k, v, state, g, beta, out, new_state, batch, k_heads,
+                     v_heads, key_dim, value_dim, 1, q_scale, stream);
 }

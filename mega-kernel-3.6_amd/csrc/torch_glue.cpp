@@ -356,34 +356,42 @@ void check_gated_delta(const torch::Tensor& q, const torch::Tensor& k, const tor
   TORCH_CHECK(g.numel() == batch * hv && beta.numel() == batch * hv, "g and beta must be [batch, value_heads]");
 }
 
-std::tuple<torch::Tensor, torch::Tensor> gated_delta_decode(torch::Tensor q, torch::Tensor k, torch::Tensor v,
-                                                            torch::Tensor state, torch::Tensor g, torch::Tensor beta) {
+// Runs the gated delta rule with the new state in `new_state` (may be
+// `state` itself); with qk_l2norm, q and k are L2-normalised in the kernel and
+// q is scaled by q_scale.
+torch::Tensor gated_delta_call(const char* fn, torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor state,
+                               torch::Tensor g, torch::Tensor beta, torch::Tensor new_state, bool qk_l2norm,
+                               double q_scale) {
   check_gated_delta(q, k, v, state, g, beta);
   c10::DeviceGuard guard(q.device());
   auto out = torch::empty({v.size(0), v.size(1), v.size(2)}, q.options());
+  const int dtype = to_mkq_dtype(q);
+  const int b = static_cast<int>(q.size(0)), hk = static_cast<int>(q.size(1)), hv = static_cast<int>(v.size(1));
+  const int dk = static_cast<int>(q.size(2)), dv = static_cast<int>(v.size(2));
+  const int rc =
+      qk_l2norm ? mkq_gated_delta_decode_qknorm(dtype, q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr<float>(),
+                                                g.data_ptr<float>(), beta.data_ptr<float>(), out.data_ptr(),
+                                                new_state.data_ptr<float>(), b, hk, hv, dk, dv,
+                                                static_cast<float>(q_scale), current_stream())
+                : mkq_gated_delta_decode(dtype, q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr<float>(),
+                                         g.data_ptr<float>(), beta.data_ptr<float>(), out.data_ptr(),
+                                         new_state.data_ptr<float>(), b, hk, hv, dk, dv, current_stream());
+  check_status(rc, fn);
+  return out;
+}
+
+std::tuple<torch::Tensor, torch::Tensor> gated_delta_decode(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                                            torch::Tensor state, torch::Tensor g, torch::Tensor beta,
+                                                            bool qk_l2norm, double q_scale) {
   auto new_state = torch::empty_like(state);
-  const int rc = mkq_gated_delta_decode(
-      to_mkq_dtype(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr<float>(), g.data_ptr<float>(),
-      beta.data_ptr<float>(), out.data_ptr(), new_state.data_ptr<float>(), static_cast<int>(q.size(0)),
-      static_cast<int>(q.size(1)), static_cast<int>(v.size(1)), static_cast<int>(q.size(2)),
-      static_cast<int>(v.size(2)), current_stream());
-  check_status(rc, "gated_delta_decode");
+  auto out = gated_delta_call("gated_delta_decode", q, k, v, state, g, beta, new_state, qk_l2norm, q_scale);
   return std::make_tuple(out, new_state);
 }
 
 // In-place variant: state is updated where it lies; returns out.
 torch::Tensor gated_delta_decode_(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor state,
-                                  torch::Tensor g, torch::Tensor beta) {
-  check_gated_delta(q, k, v, state, g, beta);
-  c10::DeviceGuard guard(q.device());
-  auto out = torch::empty({v.size(0), v.size(1), v.size(2)}, q.options());
-  const int rc = mkq_gated_delta_decode(
-      to_mkq_dtype(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), state.data_ptr<float>(), g.data_ptr<float>(),
-      beta.data_ptr<float>(), out.data_ptr(), state.data_ptr<float>(), static_cast<int>(q.size(0)),
-      static_cast<int>(q.size(1)), static_cast<int>(v.size(1)), static_cast<int>(q.size(2)),
-      static_cast<int>(v.size(2)), current_stream());
-  check_status(rc, "gated_delta_decode_");
-  return out;
+                                  torch::Tensor g, torch::Tensor beta, bool qk_l2norm, double q_scale) {
+  return gated_delta_call("gated_delta_decode_", q, k, v, state, g, beta, state, qk_l2norm, q_scale);
 }
 
 torch::Tensor gemv(torch::Tensor x, torch::Tensor w, c10::optional<torch::Tensor> residual) {
@@ -446,8 +454,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("v_new"), pybind11::arg("k_cache"), pybind11::arg("v_cache"), pybind11::arg("seq_len"),
         pybind11::arg("scale"), pybind11::arg("cos_sin") = pybind11::none(), pybind11::arg("rotary_dim") = 0);
   m.def("linear_attention_decode", &linear_attention_decode, "Recurrent linear-attention decode (HIP)");
-  m.def("gated_delta_decode", &gated_delta_decode, "Gated delta rule decode (HIP)");
-  m.def("gated_delta_decode_", &gated_delta_decode_, "Gated delta rule decode, state updated in place (HIP)");
+  m.def("gated_delta_decode", &gated_delta_decode, "Gated delta rule decode (HIP)", pybind11::arg("q"),
+        pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("state"), pybind11::arg("g"), pybind11::arg("beta"),
+        pybind11::arg("qk_l2norm") = false, pybind11::arg("q_scale") = 1.0);
+  m.def("gated_delta_decode_", &gated_delta_decode_, "Gated delta rule decode, state updated in place (HIP)",
+        pybind11::arg("q"), pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("state"), pybind11::arg("g"),
+        pybind11::arg("beta"), pybind11::arg("qk_l2norm") = false, pybind11::arg("q_scale") = 1.0);
   m.def("gemv", &gemv, "y = x w^T (+ residual) (HIP)", pybind11::arg("x"), pybind11::arg("w"),
         pybind11::arg("residual") = pybind11::none());
   m.def("gemv_add", &gemv_add, "(y, residual + y) with y = x w^T (HIP)", pybind11::arg("x"), pybind11::arg("w"),

@@ -48,6 +48,8 @@ SIGNATURES = {
         _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _i, _vp, _sz, _vp]),
     "mkq_linear_attention_decode": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     "mkq_gated_delta_decode": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "mkq_gated_delta_decode_qknorm": (
+        _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "mkq_gemv": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mkq_gemv_add": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }

@@ -109,6 +109,10 @@ class LinearAttentionInputs:
     g: Optional[torch.Tensor] = None      # [batch, v_heads] f32: selects the gated delta rule
     beta: Optional[torch.Tensor] = None   # [batch, v_heads] f32
     out_proj: Optional[torch.Tensor] = None  # [hidden, v_heads*value_dim], used by decode_layer
+    # Gated rule only: L2-normalise q and k inside the kernel (FP32) and scale
+    # q by q_scale (default 1/sqrt(key_dim)), as use_qk_l2norm_in_kernel does.
+    qk_l2norm: bool = False
+    q_scale: Optional[float] = None
 
 
 @dataclass(frozen=True)
@@ -390,13 +394,17 @@ def linear_attention_decode(inputs: LinearAttentionInputs) -> tuple[torch.Tensor
     """One recurrent step.  Returns ``(out, new_state)``; the input state is not modified.
 
     Without ``g``/``beta``: the reference rule ``S' = decay*S + k v^T``, ``o = q^T S'``.
-    With them: the gated delta rule (v head j reads q/k head ``j // (Hv // Hk)``).
+    With them: the gated delta rule (v head j reads q/k head ``j // (Hv // Hk)``);
+    ``qk_l2norm`` L2-normalises q and k inside the kernel and scales q.
     """
     if (inputs.g is None) != (inputs.beta is None):
         raise ValueError("g and beta must be given together")
+    if inputs.qk_l2norm and inputs.g is None:
+        raise ValueError("qk_l2norm needs the gated delta rule (g and beta)")
     tensors = (inputs.q, inputs.k, inputs.v, inputs.state)
     if inputs.g is not None:
         _require_extension("linear_attention_decode", *tensors, inputs.g, inputs.beta)
+        q_scale = inputs.q_scale if inputs.q_scale is not None else 1.0 / math.sqrt(inputs.q.shape[-1])
         return _C.gated_delta_decode(
             inputs.q.contiguous(),
             inputs.k.contiguous(),
@@ -404,6 +412,8 @@ def linear_attention_decode(inputs: LinearAttentionInputs) -> tuple[torch.Tensor
             inputs.state.contiguous(),
             inputs.g.float().contiguous(),
             inputs.beta.float().contiguous(),
+            qk_l2norm=bool(inputs.qk_l2norm),
+            q_scale=float(q_scale),
         )
     _require_extension("linear_attention_decode", *tensors)
     return _C.linear_attention_decode(

@@ -289,7 +289,7 @@ def linear_attention_decode(q, k, v, state, *, decay: float = 1.0):
     return out, new_state
 
 
-def gated_delta_decode(q, k, v, state, g, beta):
+def gated_delta_decode(q, k, v, state, g, beta, qk_l2norm=False, q_scale=None):
     """Gated delta rule, one decode step (the task's config-5 formula).
 
     Per batch row b and v-head j (q/k head ``h = j // (Hv // Hk)``)::
@@ -299,11 +299,21 @@ def gated_delta_decode(q, k, v, state, g, beta):
         S  <- S + beta[b,j] * k[b,h] (x) u
         o  <- S^T q[b,h]
 
-    No 1/sqrt(Dk) scale is applied to q (a caller folds it into q).
+    No 1/sqrt(Dk) scale is applied to q (a caller folds it into q), unless
+    ``qk_l2norm``: then q and k are first L2-normalised in FP32,
+    x / sqrt(sum x^2 + 1e-6) over Dk, and q is multiplied by ``q_scale``
+    (default 1/sqrt(Dk)) -- the ``use_qk_l2norm_in_kernel`` form of
+    transformers' ``torch_recurrent_gated_delta_rule`` (modeling_qwen3_next.py
+    l2norm and scale, transformers 5.15.0).
     q/k [B,Hk,Dk]; v [B,Hv,Dv]; state [B,Hv,Dk,Dv] f32; g/beta [B,Hv] f32.
     Returns (o [B,Hv,Dv] f32, new_state f32).
     """
     qf, kf, vf = as_f32(q), as_f32(k), as_f32(v)
+    if qk_l2norm:
+        dk = qf.shape[-1]
+        scale = np.float32(1.0 / np.sqrt(dk) if q_scale is None else q_scale)
+        qf = (qf / np.sqrt((qf * qf).sum(-1, keepdims=True) + np.float32(1e-6)) * scale).astype(np.float32)
+        kf = (kf / np.sqrt((kf * kf).sum(-1, keepdims=True) + np.float32(1e-6))).astype(np.float32)
     s = as_f32(state).copy()
     g = as_f32(g)
     beta = as_f32(beta)
@@ -410,6 +420,9 @@ PINNING = {
     "full_attention_decode": "F.scaled_dot_product_attention(enable_gqa=True); T=1 => out=v; constant K => mean(V)",
     "linear_attention_decode": "decay=0 => S'=k v^T; closed-form o=(q.k) v + decay q^T S",
     "gated_delta_decode": "beta=0 => S'=e^g S; g=0,beta=0 => S'=S; |k|=1,beta=1 => S'^T k = v; "
-                          "S=0,beta=1 => S'=k v^T; transformers' recurrent gated delta rule loop",
+                          "S=0,beta=1 => S'=k v^T; transformers' recurrent gated delta rule loop; "
+                          "qk_l2norm: output invariant under positive scaling of q and k, beta=1 => "
+                          "S'^T (k/|k|) = v for any k, S=0,beta=1 => o = scale cos(q,k) v, and the "
+                          "transformers loop with use_qk_l2norm_in_kernel",
     "decode_layer": "composition of pinned ops; dispatch errors match ops.py:720-739",
 }

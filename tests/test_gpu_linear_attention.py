@@ -83,3 +83,42 @@ def test_gated_delta_invariants_on_gpu():
     kk = k32.repeat_interleave(2, dim=1)  # v head j reads k head j // 2
     stk = torch.einsum("bhd,bhdv->bhv", kk, s)
     torch.testing.assert_close(stk.cpu(), inp.v.float().cpu(), atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("batch,hk,hv,dk,dv,q_scale", [
+    (1, 16, 32, 128, 128, None),   # config 5, default scale 1/sqrt(128)
+    (8, 16, 32, 128, 128, None),
+    (2, 2, 4, 64, 200, 0.3),       # ragged value columns
+    (3, 1, 3, 256, 40, None),      # key_dim at the kernel's maximum
+    (1, 2, 2, 40, 64, 1.0),        # key_dim below one wave
+])
+def test_gated_delta_qk_l2norm_in_kernel(batch, hk, hv, dk, dv, q_scale):
+    """q and k of arbitrary length, L2-normalised inside the kernel (FP32)
+    and q scaled: output and state against the oracle's qk_l2norm form, and
+    the in-place entry point agrees with the functional one bit for bit."""
+    inp = make_gated_delta(batch=batch, k_heads=hk, v_heads=hv, key_dim=dk, value_dim=dv, seed=dk + dv)
+    g = torch.Generator().manual_seed(batch * 31 + dk)
+    fq = (torch.rand(batch, hk, 1, generator=g) * 5 + 0.2).to("cuda")
+    fk = (torch.rand(batch, hk, 1, generator=g) * 5 + 0.2).to("cuda")
+    q = (inp.q.float() * fq).to(inp.q.dtype)
+    k = (inp.k.float() * fk).to(inp.k.dtype)
+    normed = mk.LinearAttentionInputs(q=q, k=k, v=inp.v, state=inp.state, g=inp.g, beta=inp.beta, qk_l2norm=True,
+                                      q_scale=q_scale)
+    out, new_state = mk.linear_attention_decode(normed)
+    ref_out, ref_state = oracle.gated_delta_decode(np32(q), np32(k), np32(inp.v), np32(inp.state), np32(inp.g),
+                                                   np32(inp.beta), qk_l2norm=True, q_scale=q_scale)
+    assert_close_out(out, ref_out)
+    assert_close_state(new_state, ref_state)
+    st = inp.state.clone()
+    scale = q_scale if q_scale is not None else dk ** -0.5
+    out2 = mk._C.gated_delta_decode_(q, k, inp.v, st, inp.g, inp.beta, qk_l2norm=True, q_scale=scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    assert torch.equal(new_state, st)
+
+
+def test_gated_delta_qk_l2norm_requires_gated_rule():
+    inp = make_linear_reference_rule()
+    with pytest.raises(ValueError, match="qk_l2norm"):
+        mk.linear_attention_decode(mk.LinearAttentionInputs(q=inp.q, k=inp.k, v=inp.v, state=inp.state,
+                                                            qk_l2norm=True))

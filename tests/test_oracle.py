@@ -267,6 +267,43 @@ def test_gated_delta_matches_transformers_recurrent_rule():
     np.testing.assert_allclose(s2, state.float().numpy(), rtol=1e-5, atol=1e-6)
 
 
+def test_gated_delta_qk_l2norm_invariants():
+    """In-kernel q/k L2 normalisation: outputs do not change when q and k are
+    scaled by positive factors; with beta = 1 the new state maps the unit key
+    to v for keys of any length; from S = 0 with beta = 1 the output is
+    scale * cos(q, k) * v."""
+    b, hk, hv, dk, dv = 2, 2, 4, 16, 6
+    q, k, v = randn(b, hk, dk), randn(b, hk, dk), randn(b, hv, dv)
+    s, g, beta = randn(b, hv, dk, dv), -np.abs(randn(b, hv)), np.abs(randn(b, hv)) % 1
+    o1, s1 = oracle.gated_delta_decode(q, k, v, s, g, beta, qk_l2norm=True)
+    o2, s2 = oracle.gated_delta_decode(q * 7.5, k * 0.5, v, s, g, beta, qk_l2norm=True)
+    np.testing.assert_allclose(o2, o1, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(s2, s1, rtol=1e-4, atol=1e-5)
+    o_raw, _ = oracle.gated_delta_decode(q, k, v, s, g, beta)
+    assert not np.allclose(o_raw, o1, rtol=1e-2)  # the flag changes the result
+    ku = np.repeat(_unit(k), hv // hk, axis=1)
+    _, s3 = oracle.gated_delta_decode(q, k * 3.0, v, s, g, np.ones_like(beta), qk_l2norm=True)
+    np.testing.assert_allclose(np.einsum("bhd,bhdv->bhv", ku, s3), v, rtol=1e-4, atol=1e-4)
+    o4, _ = oracle.gated_delta_decode(q, k, v, np.zeros_like(s), g, np.ones_like(beta), qk_l2norm=True, q_scale=0.5)
+    cos = np.repeat((_unit(q) * _unit(k)).sum(-1), hv // hk, axis=1)
+    np.testing.assert_allclose(o4, 0.5 * cos[..., None] * v, rtol=1e-4, atol=1e-5)
+
+
+def test_gated_delta_qk_l2norm_matches_transformers():
+    tr = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    b, hk, hv, dk, dv = 2, 2, 4, 16, 8
+    q, k, v = randn(b, hk, dk), randn(b, hk, dk) * 3.0, randn(b, hv, dv)
+    s, g, beta = randn(b, hv, dk, dv, scale=0.1), -np.abs(randn(b, hv)), 1 / (1 + np.exp(-randn(b, hv)))
+    o, s2 = oracle.gated_delta_decode(q, k, v, s, g, beta.astype(np.float32), qk_l2norm=True)
+    rep = hv // hk
+    out, state = tr.torch_recurrent_gated_delta_rule(
+        torch.from_numpy(np.repeat(q, rep, 1))[:, None], torch.from_numpy(np.repeat(k, rep, 1))[:, None],
+        torch.from_numpy(v)[:, None], torch.from_numpy(g)[:, None], torch.from_numpy(beta.astype(np.float32))[:, None],
+        torch.from_numpy(s), True, use_qk_l2norm_in_kernel=True)
+    np.testing.assert_allclose(o, out[:, 0].float().numpy(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(s2, state.float().numpy(), rtol=1e-5, atol=1e-5)
+
+
 # ---------------------------------------------------------------------------
 # golden vectors
 # ---------------------------------------------------------------------------
