@@ -296,6 +296,8 @@ def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
 def bench_linear(mk, inputs, timer, steps, warmup, batches):
     import dataclasses
 
+    import torch
+
     out = {}
     for b in batches:
         inp = inputs.make_gated_delta(batch=b)
@@ -311,6 +313,28 @@ def bench_linear(mk, inputs, timer, steps, warmup, batches):
         out[f"linear_qknorm_b{b}"] = r
         log(f"linear b={b} with q/k L2 norm in the kernel: {r['median_us']:.2f} us cold in stream, "
             f"{r['warm_median_us']:.2f} us warm")
+        # The whole Qwen3.6 linear-attention step around the recurrence: conv
+        # update over the 8192 q/k/v channels, the recurrence with q/k L2 norm,
+        # and the gated RMS norm of the output.
+        gen = torch.Generator().manual_seed(77)
+        conv_w = (torch.randn(8192, 4, generator=gen) * 0.3).to("cuda", torch.bfloat16)
+        conv_st = torch.randn(b, 8192, 3, generator=gen).to("cuda", torch.bfloat16)
+        xin = torch.randn(b, 8192, generator=gen).to("cuda", torch.bfloat16)
+        zg = torch.randn(b, 32, 128, generator=gen).to("cuda", torch.bfloat16)
+        nw = torch.ones(128, dtype=torch.bfloat16, device="cuda")
+
+        def step(b=b, inp=inp, conv_w=conv_w, conv_st=conv_st, xin=xin, zg=zg, nw=nw):
+            mixed = mk.causal_conv1d_update(xin, conv_st, conv_w)
+            q = mixed[:, :2048].reshape(b, 16, 128)
+            k = mixed[:, 2048:4096].reshape(b, 16, 128)
+            v = mixed[:, 4096:].reshape(b, 32, 128)
+            o, _ = mk.linear_attention_decode(dataclasses.replace(inp, q=q, k=k, v=v, qk_l2norm=True))
+            return mk.gated_rms_norm(o, zg, nw)
+
+        r = measure(timer, step, steps, warmup, linear_bytes(b, 16, 32, 128, 128) + 8192 * 4 * 2 + b * 8192 * 3 * 4)
+        out[f"linear_step_b{b}"] = r
+        log(f"linear step b={b} (conv update + recurrence with q/k norm + gated norm): "
+            f"{r['median_us']:.2f} us cold in stream, {r['warm_median_us']:.2f} us warm")
     return out
 
 

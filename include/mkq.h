@@ -176,6 +176,30 @@ int mkq_gated_delta_decode_qknorm(int dtype, const void* q, const void* k, const
                                   int value_dim, float q_scale, void* stream);
 
 /* ------------------------------------------------------------------------
+ * The ops around the gated delta recurrence in the Qwen3.6 linear-attention
+ * decode step.  No counterpart in the reference; they restate the model's
+ * causal_conv1d_update and RMSNormGated (transformers 5.15.0,
+ * modeling_qwen3_next.py).
+ *
+ * mkq_causal_conv1d_update: one new token per channel through a depthwise
+ * causal convolution of width state_len + 1.  x [batch, channels];
+ * conv_state [batch, channels, state_len] (dtype, updated in place: it keeps
+ * the last state_len inputs); weight [channels, state_len + 1]; bias
+ * [channels] or NULL; out [batch, channels] = silu(conv) (or conv when
+ * silu_activation is 0).  The convolution is rounded to dtype before the SiLU.
+ * state_len <= 7.
+ *
+ * mkq_gated_rms_norm: per row of dim values, n = round(x * rsqrt(mean(x^2) +
+ * eps)) (FP32 mean and rsqrt), t = round(weight * n), out = round(t *
+ * silu(gate)).  x, gate, out [rows, dim]; weight [dim].
+ * ---------------------------------------------------------------------- */
+int mkq_causal_conv1d_update(int dtype, const void* x, void* conv_state, const void* weight,
+                             const void* bias, void* out, int batch, int channels, int state_len,
+                             int silu_activation, void* stream);
+int mkq_gated_rms_norm(int dtype, const void* x, const void* gate, const void* weight, void* out,
+                       int rows, int dim, float eps, void* stream);
+
+/* ------------------------------------------------------------------------
  * Plain GEMV used for the optional attention output projections in
  * decode_layer: y[b, n] = sum_k w[n, k] * x[b, k] (+ residual[b, n]).
  * No counterpart in the reference (decode_layer reshapes, ops.py:722,728).

@@ -394,6 +394,55 @@ torch::Tensor gated_delta_decode_(torch::Tensor q, torch::Tensor k, torch::Tenso
   return gated_delta_call("gated_delta_decode_", q, k, v, state, g, beta, state, qk_l2norm, q_scale);
 }
 
+// x [batch, channels]; conv_state [batch, channels, state_len] updated in
+// place; weight [channels, state_len + 1]; returns act(conv) [batch, channels].
+torch::Tensor causal_conv1d_update(torch::Tensor x, torch::Tensor conv_state, torch::Tensor weight,
+                                   c10::optional<torch::Tensor> bias, bool silu_activation) {
+  MK_CHECK_INPUT(x);
+  MK_CHECK_INPUT(conv_state);
+  MK_CHECK_INPUT(weight);
+  TORCH_CHECK(x.dim() == 2, "x must be [batch, channels]");
+  TORCH_CHECK(conv_state.dim() == 3 && conv_state.size(0) == x.size(0) && conv_state.size(1) == x.size(1),
+              "conv_state must be [batch, channels, state_len]");
+  TORCH_CHECK(weight.dim() == 2 && weight.size(0) == x.size(1) && weight.size(1) == conv_state.size(2) + 1,
+              "weight must be [channels, state_len + 1]");
+  TORCH_CHECK(x.scalar_type() == conv_state.scalar_type() && x.scalar_type() == weight.scalar_type(),
+              "x, conv_state and weight dtype mismatch");
+  const void* b = nullptr;
+  if (bias.has_value()) {
+    MK_CHECK_INPUT((*bias));
+    TORCH_CHECK(bias->numel() == x.size(1) && bias->scalar_type() == x.scalar_type(), "bias must be [channels]");
+    b = bias->data_ptr();
+  }
+  c10::DeviceGuard guard(x.device());
+  auto out = torch::empty_like(x);
+  const int rc = mkq_causal_conv1d_update(to_mkq_dtype(x), x.data_ptr(), conv_state.data_ptr(), weight.data_ptr(), b,
+                                          out.data_ptr(), static_cast<int>(x.size(0)), static_cast<int>(x.size(1)),
+                                          static_cast<int>(conv_state.size(2)), silu_activation ? 1 : 0,
+                                          current_stream());
+  check_status(rc, "causal_conv1d_update");
+  return out;
+}
+
+// x, gate [..., dim]; weight [dim]: weight * rms_norm(x) * silu(gate).
+torch::Tensor gated_rms_norm(torch::Tensor x, torch::Tensor gate, torch::Tensor weight, double eps) {
+  MK_CHECK_INPUT(x);
+  MK_CHECK_INPUT(gate);
+  MK_CHECK_INPUT(weight);
+  TORCH_CHECK(x.dim() >= 1 && gate.sizes() == x.sizes(), "gate shape must match x");
+  TORCH_CHECK(weight.dim() == 1 && weight.size(0) == x.size(-1), "weight must be [dim]");
+  TORCH_CHECK(x.scalar_type() == gate.scalar_type() && x.scalar_type() == weight.scalar_type(),
+              "x, gate and weight dtype mismatch");
+  c10::DeviceGuard guard(x.device());
+  auto out = torch::empty_like(x);
+  const int64_t dim = x.size(-1);
+  const int rc = mkq_gated_rms_norm(to_mkq_dtype(x), x.data_ptr(), gate.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                                    static_cast<int>(x.numel() / dim), static_cast<int>(dim),
+                                    static_cast<float>(eps), current_stream());
+  check_status(rc, "gated_rms_norm");
+  return out;
+}
+
 torch::Tensor gemv(torch::Tensor x, torch::Tensor w, c10::optional<torch::Tensor> residual) {
   MK_CHECK_INPUT(x);
   MK_CHECK_INPUT(w);
@@ -460,6 +509,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gated_delta_decode_", &gated_delta_decode_, "Gated delta rule decode, state updated in place (HIP)",
         pybind11::arg("q"), pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("state"), pybind11::arg("g"),
         pybind11::arg("beta"), pybind11::arg("qk_l2norm") = false, pybind11::arg("q_scale") = 1.0);
+  m.def("causal_conv1d_update", &causal_conv1d_update, "Causal conv1d state update for one token (HIP)",
+        pybind11::arg("x"), pybind11::arg("conv_state"), pybind11::arg("weight"),
+        pybind11::arg("bias") = pybind11::none(), pybind11::arg("silu_activation") = true);
+  m.def("gated_rms_norm", &gated_rms_norm, "Gated RMS norm, norm before gate (HIP)", pybind11::arg("x"),
+        pybind11::arg("gate"), pybind11::arg("weight"), pybind11::arg("eps") = 1e-6);
   m.def("gemv", &gemv, "y = x w^T (+ residual) (HIP)", pybind11::arg("x"), pybind11::arg("w"),
         pybind11::arg("residual") = pybind11::none());
   m.def("gemv_add", &gemv_add, "(y, residual + y) with y = x w^T (HIP)", pybind11::arg("x"), pybind11::arg("w"),

@@ -20,10 +20,12 @@ from .ops import (
     LinearAttentionInputs,
     MoeWeights,
     apply_partial_rope,
+    causal_conv1d_update,
     decode_layer,
     dense_ffn_decode,
     extension_available,
     full_attention_decode,
+    gated_rms_norm,
     linear_attention_decode,
     moe_decode,
 )
@@ -38,10 +40,12 @@ __all__ = [
     "MoeWeights",
     "Qwen36TextConfig",
     "apply_partial_rope",
+    "causal_conv1d_update",
     "decode_layer",
     "dense_ffn_decode",
     "extension_available",
     "full_attention_decode",
+    "gated_rms_norm",
     "library_path",
     "linear_attention_decode",
     "load_library",

@@ -50,6 +50,8 @@ SIGNATURES = {
     "mkq_gated_delta_decode": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "mkq_gated_delta_decode_qknorm": (
         _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
+    "mkq_causal_conv1d_update": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "mkq_gated_rms_norm": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "mkq_gemv": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mkq_gemv_add": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }

@@ -390,6 +390,40 @@ def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:
     return _C.full_attention_decode(q.contiguous(), k_cache.contiguous(), inputs.v_cache.contiguous(), float(scale))
 
 
+def causal_conv1d_update(
+    x: torch.Tensor,
+    conv_state: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    activation: Optional[str] = "silu",
+) -> torch.Tensor:
+    """One token through the depthwise causal convolution in front of the
+    Qwen3.6 linear-attention recurrence (the model's causal_conv1d_update,
+    kernel width 4): x [batch, channels] (or [batch, channels, 1]),
+    conv_state [batch, channels, width - 1] updated in place, weight
+    [channels, width] (or [channels, 1, width]).  Returns act(conv) shaped like
+    x.  No counterpart in the reference."""
+    if activation not in (None, "silu", "swish"):
+        raise ValueError(f"unsupported activation: {activation}")
+    _require_extension("causal_conv1d_update", x, conv_state, weight)
+    if not conv_state.is_contiguous():
+        raise ValueError("conv_state must be contiguous: it is updated in place")
+    w = weight.reshape(weight.shape[0], weight.shape[-1]).contiguous()
+    out = _C.causal_conv1d_update(x.reshape(x.shape[0], -1).contiguous(), conv_state, w,
+                                  None if bias is None else bias.contiguous(), activation is not None)
+    return out.reshape(x.shape)
+
+
+def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """weight * rms_norm(x) * silu(gate) over the last dimension, norm before
+    gate, with the roundings of the model's RMSNormGated: the normalised x
+    and the weighted value are rounded to x's dtype, the mean and rsqrt are
+    FP32.  The output norm of the Qwen3.6 linear-attention step.  No
+    counterpart in the reference."""
+    _require_extension("gated_rms_norm", x, gate, weight)
+    return _C.gated_rms_norm(x.contiguous(), gate.contiguous(), weight.contiguous(), float(eps))
+
+
 def linear_attention_decode(inputs: LinearAttentionInputs) -> tuple[torch.Tensor, torch.Tensor]:
     """One recurrent step.  Returns ``(out, new_state)``; the input state is not modified.
 

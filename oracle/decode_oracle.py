@@ -53,6 +53,8 @@ __all__ = [
     "full_attention_decode",
     "linear_attention_decode",
     "gated_delta_decode",
+    "causal_conv1d_update",
+    "gated_rms_norm",
     "decode_layer",
     "PINNING",
 ]
@@ -334,6 +336,41 @@ def gated_delta_decode(q, k, v, state, g, beta, qk_l2norm=False, q_scale=None):
     return out, s.astype(np.float32)
 
 
+def causal_conv1d_update(x, conv_state, weight, bias=None, *, silu_activation=True, bf16=True):
+    """One token through the depthwise causal convolution of the Qwen3.6
+    linear-attention step (transformers 5.15.0 ``causal_conv1d_update``,
+    modeling_qwen3_next.py: window = [state, x], conv over the window, SiLU,
+    state <- window[1:]).  x [B, C]; conv_state [B, C, S]; weight [C, S+1];
+    bias [C] or None.  With ``bf16`` the convolution and the SiLU are each
+    rounded to bfloat16, as the model's bf16 ops round them.
+    Returns (out [B, C] f32, new_state [B, C, S] f32)."""
+    xf = as_f32(x)
+    st = as_f32(conv_state)
+    w = as_f32(weight)
+    win = np.concatenate([st, xf[..., None]], axis=-1)                      # [B, C, S+1]
+    acc = (win.astype(np.float64) * w.astype(np.float64)[None]).sum(-1).astype(np.float32)
+    if bias is not None:
+        acc = (acc + as_f32(bias)[None]).astype(np.float32)
+    rnd = bf16_round if bf16 else (lambda a: a.astype(np.float32))
+    y = rnd(acc)
+    if silu_activation:
+        y = rnd(silu(y))
+    return y, win[..., 1:].astype(np.float32)
+
+
+def gated_rms_norm(x, gate, weight, *, eps=1e-6, bf16=True):
+    """Norm-before-gate RMSNorm of the Qwen3.6 linear-attention output
+    (transformers 5.15.0 ``Qwen3NextRMSNormGated.forward``): n = x *
+    rsqrt(mean(x^2) + eps) in FP32, rounded to the input dtype; t = weight * n
+    rounded; out = t * silu(gate) in FP32, rounded."""
+    rnd = bf16_round if bf16 else (lambda a: a.astype(np.float32))
+    xf = as_f32(x)
+    var = np.mean(xf * xf, axis=-1, keepdims=True, dtype=np.float32)
+    n = rnd(xf * (np.float32(1.0) / np.sqrt(var + np.float32(eps))))
+    t = rnd(as_f32(weight) * n)
+    return rnd(t * silu(as_f32(gate)))
+
+
 # ---------------------------------------------------------------------------
 # decode_layer composition  (ops.py:701-748)
 # ---------------------------------------------------------------------------
@@ -424,5 +461,9 @@ PINNING = {
                           "qk_l2norm: output invariant under positive scaling of q and k, beta=1 => "
                           "S'^T (k/|k|) = v for any k, S=0,beta=1 => o = scale cos(q,k) v, and the "
                           "transformers loop with use_qk_l2norm_in_kernel",
+    "causal_conv1d_update": "transformers' causal_conv1d_update (torch conv1d) on float32 and bfloat16; last-tap weight 1 "
+                            "and no activation => out = x and the state shifts by one",
+    "gated_rms_norm": "transformers' Qwen3NextRMSNormGated on float32 and bfloat16; constant rows => "
+                      "weight * sign(x) * silu(gate)",
     "decode_layer": "composition of pinned ops; dispatch errors match ops.py:720-739",
 }

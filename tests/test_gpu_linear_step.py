@@ -1,0 +1,97 @@
+"""GPU parity: the ops around the gated delta recurrence in the Qwen3.6
+linear-attention step -- the causal conv1d state update (width 4, SiLU) and
+the gated RMS norm on the output -- against the oracle's restatements, which
+are pinned against transformers' own functions on the CPU.
+
+Tolerances (task): bf16 outputs atol/rtol 1e-2; the conv state is a copy of
+inputs and must match bit for bit.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import mega_kernel_qwen36 as mk
+import oracle
+from mega_kernel_qwen36 import _lib
+from tests.inputs import assert_close_out, np32
+
+pytestmark = pytest.mark.gpu
+
+# Qwen3.6-35B-A3B: q and k 16 heads x 128, v 32 heads x 128 -> 8192 conv channels.
+QWEN_CHANNELS = 2 * 16 * 128 + 32 * 128
+
+
+def _rand(shape, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to("cuda", dtype)
+
+
+@pytest.mark.parametrize("batch,channels,state_len,dtype,bias,act", [
+    (1, QWEN_CHANNELS, 3, torch.bfloat16, False, True),
+    (8, QWEN_CHANNELS, 3, torch.bfloat16, False, True),
+    (3, 1000, 3, torch.float16, True, True),
+    (2, 300, 5, torch.float32, True, False),
+    (1, 64, 1, torch.bfloat16, False, True),
+])
+def test_causal_conv1d_update(batch, channels, state_len, dtype, bias, act):
+    x = _rand((batch, channels), 1 + channels, dtype)
+    st = _rand((batch, channels, state_len), 2 + channels, dtype)
+    w = _rand((channels, state_len + 1), 3 + channels, dtype, 0.5)
+    b = _rand((channels,), 4 + channels, dtype) if bias else None
+    ref_out, ref_state = oracle.causal_conv1d_update(np32(x), np32(st), np32(w), None if b is None else np32(b),
+                                                     silu_activation=act, bf16=dtype == torch.bfloat16)
+    out = mk.causal_conv1d_update(x, st, w, b, activation="silu" if act else None)
+    torch.cuda.synchronize()
+    assert out.shape == x.shape and out.dtype == dtype
+    assert_close_out(out, ref_out)
+    np.testing.assert_array_equal(np32(st), ref_state)  # the window shifted by one token
+
+
+def test_causal_conv1d_update_two_steps_through_c_abi():
+    """Two tokens in a row through mkq_causal_conv1d_update: the second step
+    convolves over the state the first one left."""
+    lib = _lib.load_library()
+    b, c, sl = 2, QWEN_CHANNELS, 3
+    st = _rand((b, c, sl), 11, torch.bfloat16)
+    w = _rand((c, sl + 1), 12, torch.bfloat16, 0.5)
+    ref_state = np32(st)
+    for step in range(2):
+        x = _rand((b, c), 13 + step, torch.bfloat16)
+        out = torch.empty_like(x)
+        rc = lib.mkq_causal_conv1d_update(_lib.MKQ_DTYPE_BF16, x.data_ptr(), st.data_ptr(), w.data_ptr(), None,
+                                          out.data_ptr(), b, c, sl, 1, torch.cuda.current_stream().cuda_stream)
+        assert rc == _lib.MKQ_OK, lib.mkq_last_error()
+        torch.cuda.synchronize()
+        ref_out, ref_state = oracle.causal_conv1d_update(np32(x), ref_state, np32(w))
+        assert_close_out(out, ref_out)
+        np.testing.assert_array_equal(np32(st), ref_state)
+
+
+@pytest.mark.parametrize("rows,dim,dtype", [
+    (32, 128, torch.bfloat16),     # config 5 at batch 1: 32 v heads of 128
+    (256, 128, torch.bfloat16),    # batch 8
+    (7, 100, torch.float16),       # dim not a multiple of the wave
+    (5, 384, torch.float32),
+])
+def test_gated_rms_norm(rows, dim, dtype):
+    x = _rand((rows, dim), 21 + dim, dtype)
+    z = _rand((rows, dim), 22 + dim, dtype, 2.0)
+    w = _rand((dim,), 23 + dim, dtype, 0.3) + 1.0
+    out = mk.gated_rms_norm(x, z, w, eps=1e-6)
+    torch.cuda.synchronize()
+    ref = oracle.gated_rms_norm(np32(x), np32(z), np32(w), eps=1e-6, bf16=dtype == torch.bfloat16)
+    assert out.shape == x.shape and out.dtype == dtype
+    assert_close_out(out, ref)
+
+
+def test_gated_rms_norm_head_layout():
+    """[batch, heads, dim] input, as the linear-attention output is laid out:
+    each (batch, head) row is normalised on its own."""
+    x = _rand((2, 32, 128), 31, torch.bfloat16)
+    z = _rand((2, 32, 128), 32, torch.bfloat16)
+    w = _rand((128,), 33, torch.bfloat16, 0.3) + 1.0
+    out = mk.gated_rms_norm(x, z, w)
+    torch.cuda.synchronize()
+    ref = oracle.gated_rms_norm(np32(x).reshape(-1, 128), np32(z).reshape(-1, 128), np32(w))
+    assert_close_out(out.reshape(-1, 128), ref)

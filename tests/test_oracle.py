@@ -304,6 +304,63 @@ def test_gated_delta_qk_l2norm_matches_transformers():
     np.testing.assert_allclose(s2, state.float().numpy(), rtol=1e-5, atol=1e-5)
 
 
+def test_causal_conv1d_update_identity_tap_and_shift():
+    """With only the newest tap set to 1 and no activation the output is the
+    input, and the state shifts by one token with the input appended."""
+    b, c, sl = 2, 12, 3
+    x, st = randn(b, c), randn(b, c, sl)
+    w = np.zeros((c, sl + 1), np.float32)
+    w[:, -1] = 1.0
+    out, new_state = oracle.causal_conv1d_update(x, st, w, silu_activation=False, bf16=False)
+    np.testing.assert_array_equal(out, x)
+    np.testing.assert_array_equal(new_state, np.concatenate([st[..., 1:], x[..., None]], -1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_causal_conv1d_update_matches_transformers(dtype):
+    tr = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    b, c, sl = 2, 40, 3
+    x, st, w, bias = randn(b, c), randn(b, c, sl), randn(c, sl + 1, scale=0.5), randn(c)
+    bf = dtype == torch.bfloat16
+    if bf:
+        x, st, w, bias = (oracle.bf16_round(a) for a in (x, st, w, bias))
+    for bias_ in (None, bias):
+        out, new_state = oracle.causal_conv1d_update(x, st, w, bias_, bf16=bf)
+        ts = torch.from_numpy(st.copy()).to(dtype)
+        ref = tr.causal_conv1d_update(torch.from_numpy(x).to(dtype)[..., None], ts, torch.from_numpy(w).to(dtype),
+                                      None if bias_ is None else torch.from_numpy(bias_).to(dtype), "silu")
+        tol = 8e-3 if bf else 1e-5
+        np.testing.assert_allclose(out, ref[..., 0].float().numpy(), rtol=tol, atol=tol)
+        np.testing.assert_array_equal(new_state, ts.float().numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_rms_norm_matches_transformers(dtype):
+    tr = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    rows, d = 6, 128
+    x, z, w = randn(rows, d), randn(rows, d), randn(d, scale=0.5) + 1.0
+    bf = dtype == torch.bfloat16
+    if bf:
+        x, z, w = (oracle.bf16_round(a) for a in (x, z, w))
+    out = oracle.gated_rms_norm(x, z, w, eps=1e-6, bf16=bf)
+    mod = tr.Qwen3NextRMSNormGated(d, eps=1e-6).to(dtype)
+    with torch.no_grad():
+        mod.weight.copy_(torch.from_numpy(w).to(dtype))
+        ref = mod(torch.from_numpy(x).to(dtype), torch.from_numpy(z).to(dtype)).float().numpy()
+    tol = 8e-3 if bf else 1e-5
+    np.testing.assert_allclose(out, ref, rtol=tol, atol=tol)
+
+
+def test_gated_rms_norm_constant_rows():
+    """A constant row normalises to its sign, so out = weight * sign * silu(gate)."""
+    d = 16
+    x = np.stack([np.full(d, 3.0), np.full(d, -0.25)]).astype(np.float32)
+    z, w = randn(2, d), randn(d)
+    out = oracle.gated_rms_norm(x, z, w, eps=0.0, bf16=False)
+    silu = z / (1 + np.exp(-z))
+    np.testing.assert_allclose(out, np.sign(x) * w * silu, rtol=1e-5, atol=1e-6)
+
+
 # ---------------------------------------------------------------------------
 # golden vectors
 # ---------------------------------------------------------------------------
