@@ -140,6 +140,25 @@ int mkq_full_attention_decode_append(int dtype, const void* q, const void* k_new
                                      const float* cos_sin, int rotary_dim, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
+/* Paged KV layout: k_blocks, v_blocks [num_blocks, block_size, kv_heads,
+ * head_dim] hold the caches of all sequences in fixed-size blocks, and
+ * block_table [batch, max_blocks] (int32, device) lists each batch row's
+ * blocks in token order: token t of row b is row t % block_size of block
+ * block_table[b, t / block_size].  The result equals
+ * mkq_full_attention_decode over the gathered contiguous cache of seq_len
+ * tokens, bit for bit.  A block id outside [0, num_blocks) reads as zeros
+ * (no fault).  block_size a multiple of 16; max_blocks * block_size >=
+ * seq_len; bf16/f16, head_dim % 8 == 0 and 16-byte aligned tensors, else
+ * MKQ_ERR_UNSUPPORTED.  The workspace is sized as for the contiguous entry
+ * point.  No counterpart in the reference, whose attention reads one
+ * contiguous [B, T, Hkv, D] cache (attention_decode.cu:152-218); its task
+ * planner assumes paged attention (mpk_graph.py:383-390). */
+int mkq_full_attention_decode_paged(int dtype, const void* q, const void* k_blocks, const void* v_blocks,
+                                    const int* block_table, void* out, int batch, int q_heads,
+                                    int kv_heads, int head_dim, int seq_len, int block_size,
+                                    int max_blocks, int num_blocks, float scale, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Recurrent linear-attention decode, reference rule.  Replaces
  *   _C.linear_attention_decode    (csrc/bindings.cpp:35, csrc/linear_attention_decode.cu:46-93)

@@ -167,11 +167,18 @@ size_t chunk_lds_bytes(int d, int heads) {
 // the cache row (kw/vw, the cache pointers) at the end.  No workgroup of the
 // launch reads that cache row and uses it.  `cap` is the cache's token
 // capacity (batch stride in tokens); seq <= cap.
-template <typename T, int DT, bool ROPE, bool APP>
+//
+// PG (paged KV): kc/vc are pools of blocks [nblocks, bsz, hkv, d] and token t
+// of batch row b lives in block btab[b * maxb + t / bsz]; bsz % 16 == 0, so a
+// 16-token tile never straddles two blocks.  The chunk's block ids are staged
+// in LDS once; every tile gets a descriptor over its own rows, and an id
+// outside [0, nblocks) reads as zeros.
+template <typename T, int DT, bool ROPE, bool APP, bool PG>
 __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc, float* __restrict__ part_o,
     float* __restrict__ part_m, float* __restrict__ part_l, T* __restrict__ out, const float* __restrict__ rope_cs,
-    const T* __restrict__ k_new, const T* __restrict__ v_new, T* kw, T* vw, int cap, int rot, int rope_lds_off,
+    const T* __restrict__ k_new, const T* __restrict__ v_new, T* kw, T* vw, int cap, const int* __restrict__ btab,
+    int bsz, int maxb, int nblocks, int blk_lds_off, int rot, int rope_lds_off,
     int hq, int hkv, int d, int seq, int group, int ngroups, int units, int nch, int chunk_tokens,
     float scale_log2) {
   typedef typename Mfma<T>::vec8 V8;
@@ -183,7 +190,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   constexpr int VSTR = v_stride(DT);
   static_assert(VCH >= 1 && kTT * CPR == VCH * kWave, "V tile must split evenly over the wave");
 
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x % kWave, wave = wave_id();
   const int col = lane & 15, grp = lane >> 4;
   const int unit = blockIdx.x % units, c = blockIdx.x / units;
@@ -201,6 +207,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   const uint32_t bytes = (uint32_t(len) - 1) * tsb + uint32_t(d) * sizeof(T);
   const rsrc_t kr = make_rsrc(kc + base, bytes);
   const rsrc_t vr = make_rsrc(vc + base, bytes);
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  int* blk_l = reinterpret_cast<int*>(smem + blk_lds_off);
+  const int bi0 = PG ? t_begin / bsz : 0;
+  if constexpr (PG) {
+    const int nbl = (t_begin + len - 1) / bsz - bi0 + 1;
+    for (int i = threadIdx.x; i < nbl; i += kThreads) {
+      const int bi = bi0 + i;
+      blk_l[i] = bi < maxb ? btab[size_t(b) * maxb + bi] : -1;
+    }
+    __syncthreads();
+  }
+  // The descriptor and base offset for the 16-token tile at chunk row t
+  // (wave-uniform): the chunk-wide descriptor, or with PG one over the tile's
+  // rows in its block.  Rows past the chunk read as zeros either way.
+  auto tile_src = [&](const T* cache, const rsrc_t& whole, int t, uint32_t& ob)
+                      __attribute__((always_inline)) -> rsrc_t {
+    if constexpr (!PG) {
+      ob = uint32_t(t) * tsb;
+      return whole;
+    } else {
+      ob = 0;
+      const int rows = min(len - t, kTT);
+      if (rows <= 0) return make_rsrc(cache, 0u);
+      const int tg = t_begin + t;
+      const int blk = __builtin_amdgcn_readfirstlane(blk_l[tg / bsz - bi0]);
+      if (blk < 0 || blk >= nblocks) return make_rsrc(cache, 0u);
+      const T* p = cache + (size_t(blk) * bsz + tg % bsz) * hkv * d + size_t(kvh) * d;
+      return make_rsrc(p, uint32_t(rows - 1) * tsb + uint32_t(d) * sizeof(T));
+    }
+  };
 
   // Q^T as the B operand: lane (head col, k-group grp) holds dims 32s+8grp..+8;
   // heads past the group read zero.
@@ -263,10 +300,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
 
   u32x4 kreg[VCH], vreg[VCH];
   int t0 = wave * kTT;
+  {
+    uint32_t ob;
+    const rsrc_t rk = tile_src(kc, kr, t0, ob);
 #pragma unroll
-  for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(kr, uint32_t(t0) * tsb + voff[i]);
+    for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(rk, ob + voff[i]);
+    const rsrc_t rv = tile_src(vc, vr, t0, ob);
 #pragma unroll
-  for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, uint32_t(t0) * tsb + voff[i]);
+    for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(rv, ob + voff[i]);
+  }
   pin_loads();
 
   // ROPE, once the first tile is in flight: the cos/sin table into LDS, then
@@ -321,10 +363,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
         *reinterpret_cast<u32x4*>(rowp + c * 16) = rope8<T>(own, pq, rope_l + c * 8, rope_l + rot + c * 8);
       }
     }
-    const uint32_t next = uint32_t(t0 + kWgTokens) * tsb;
+    uint32_t nob;
     if (pf) {
+      const rsrc_t nk = tile_src(kc, kr, t0 + kWgTokens, nob);
 #pragma unroll
-      for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(kr, next + voff[i]);
+      for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(nk, nob + voff[i]);
       pin_loads();
     }
     f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -371,8 +414,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
       }
     }
     if (pf) {
+      const rsrc_t nv = tile_src(vc, vr, t0 + kWgTokens, nob);
 #pragma unroll
-      for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(vr, next + voff[i]);
+      for (int i = 0; i < VCH; ++i) vreg[i] = buf_load16<kAuxStream>(nv, nob + voff[i]);
       pin_loads();
     }
 
@@ -641,28 +685,54 @@ struct Append {
   int cap = 0;
 };
 
+// Paged launches pass the block table [batch, max_blocks] (int32), the block
+// size in tokens and the pool's block count.
+struct Paged {
+  const int* table = nullptr;
+  int block_size = 0;
+  int max_blocks = 0;
+  int num_blocks = 0;
+};
+
+// A paged chunk stages at most this many block ids in LDS.
+constexpr int kMaxChunkBlocks = 1024;
+
 template <typename T, int DT>
 int launch_fast(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
-                float scale, const float* rope_cs, int rot, const Append& ap, float* ws, hipStream_t stream) {
+                float scale, const float* rope_cs, int rot, const Append& ap, const Paged& pg, float* ws,
+                hipStream_t stream) {
   const int group = hq / hkv;
   const int ngroups = (group + 15) / 16;
   const int units = batch * hkv * ngroups;
   Chunking ch;
   const int rc = plan_chunks(units, hkv, d, seq, sizeof(T), &ch);
   if (rc != MKQ_OK) return rc;
+  const bool paged = pg.table != nullptr;
+  if (paged) {  // a chunk's block ids must fit the LDS table
+    const int cap_tokens = (kMaxChunkBlocks - 2) * pg.block_size / kWgTokens * kWgTokens;
+    if (ch.chunk_tokens > cap_tokens) {
+      ch.chunk_tokens = cap_tokens;
+      ch.nch = (seq + cap_tokens - 1) / cap_tokens;
+      if (ch.nch > kMaxChunks)
+        return set_error(MKQ_ERR_UNSUPPORTED, "full_attention_decode_paged: seq_len %d needs too many chunks", seq);
+    }
+  }
   const size_t lds = chunk_lds_bytes<DT>(d, group < 16 ? group : 16);
   static bool attr_set = false;
   if (!attr_set) {
     const int plain = int(chunk_lds_bytes<DT>(DT, 16));
     const int roped = int(chunk_lds_bytes<DT>(DT, 16) + 16 + 2 * kMaxD * sizeof(float));
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, false>),
+    const int pagedb = int(chunk_lds_bytes<DT>(DT, 16) + 16 + kMaxChunkBlocks * sizeof(int));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, false, false>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, plain));
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, false>),
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, false, false>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, roped));
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, true>),
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, true, false>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, plain));
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, true>),
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, true, false>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, roped));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, false, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, pagedb));
     attr_set = true;
   }
   MKQ_REQUIRE(size_t(ch.nch) * units < (size_t(1) << 31), "full_attention_decode: grid too large");
@@ -670,16 +740,22 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   float* part_m = part_o + size_t(batch) * hq * ch.nch * d;
   float* part_l = part_m + size_t(batch) * hq * ch.nch;
   const bool app = ap.k_new != nullptr;
-  auto* kern = rot > 0 ? (app ? attn_chunk_kernel<T, DT, true, true> : attn_chunk_kernel<T, DT, true, false>)
-                       : (app ? attn_chunk_kernel<T, DT, false, true> : attn_chunk_kernel<T, DT, false, false>);
-  const size_t rope_off = (lds + 15) / 16 * 16;  // the cos/sin table follows the staging/merge area
-  const size_t lds_all = rot > 0 ? rope_off + size_t(2 * rot) * sizeof(float) : lds;
+  auto* kern = paged  ? attn_chunk_kernel<T, DT, false, false, true>
+               : rot > 0 ? (app ? attn_chunk_kernel<T, DT, true, true, false> : attn_chunk_kernel<T, DT, true, false, false>)
+                         : (app ? attn_chunk_kernel<T, DT, false, true, false>
+                                : attn_chunk_kernel<T, DT, false, false, false>);
+  // The cos/sin table (ROPE) or the block ids (PG) follow the staging/merge area.
+  const size_t rope_off = (lds + 15) / 16 * 16;
+  const int nblk = paged ? (ch.chunk_tokens + pg.block_size - 1) / pg.block_size + 2 : 0;
+  const size_t lds_all = rot > 0 ? rope_off + size_t(2 * rot) * sizeof(float)
+                         : paged ? rope_off + size_t(nblk) * sizeof(int)
+                                 : lds;
   kern<<<dim3(ch.nch * units), kThreads, lds_all, stream>>>(
       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), part_o, part_m, part_l,
       static_cast<T*>(out), rope_cs, static_cast<const T*>(ap.k_new), static_cast<const T*>(ap.v_new),
       app ? static_cast<T*>(const_cast<void*>(k)) : nullptr, app ? static_cast<T*>(const_cast<void*>(v)) : nullptr,
-      app ? ap.cap : seq, rot, int(rope_off), hq, hkv, d, seq, group, ngroups, units, ch.nch, ch.chunk_tokens,
-      scale * kLog2e);
+      app ? ap.cap : seq, pg.table, pg.block_size, pg.max_blocks, pg.num_blocks, int(rope_off), rot, int(rope_off), hq,
+      hkv, d, seq, group, ngroups, units, ch.nch, ch.chunk_tokens, scale * kLog2e);
   MKQ_LAUNCH_CHECK("attn_chunk_kernel");
   if (ch.nch > 1) {
     dim3 g2(batch * hq, (d + kWave - 1) / kWave);
@@ -691,11 +767,13 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
 
 template <typename T>
 int launch_fast_d(const void* q, const void* k, const void* v, void* out, int batch, int hq, int hkv, int d, int seq,
-                  float scale, const float* rope_cs, int rot, const Append& ap, float* ws, hipStream_t stream) {
-  if (d <= 64) return launch_fast<T, 64>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, ws, stream);
+                  float scale, const float* rope_cs, int rot, const Append& ap, const Paged& pg, float* ws,
+                  hipStream_t stream) {
+  if (d <= 64)
+    return launch_fast<T, 64>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, pg, ws, stream);
   if (d <= 128)
-    return launch_fast<T, 128>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, ws, stream);
-  return launch_fast<T, 256>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, ws, stream);
+    return launch_fast<T, 128>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, pg, ws, stream);
+  return launch_fast<T, 256>(q, k, v, out, batch, hq, hkv, d, seq, scale, rope_cs, rot, ap, pg, ws, stream);
 }
 
 template <typename T>
@@ -724,8 +802,8 @@ namespace {
 
 int attention_entry(const char* fn, int dtype, const void* q, const void* k_cache, const void* v_cache, void* out,
                     int batch, int q_heads, int kv_heads, int head_dim, int seq_len, float scale,
-                    const float* rope_cs, int rot, const Append& ap, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+                    const float* rope_cs, int rot, const Append& ap, const Paged& pg, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   clear_error();
   MKQ_REQUIRE(batch > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0, "%s: sizes must be positive", fn);
   MKQ_REQUIRE(seq_len > 0, "seq_len must be positive");
@@ -740,6 +818,15 @@ int attention_entry(const char* fn, int dtype, const void* q, const void* k_cach
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* ws = static_cast<float*>(workspace);
   const bool fast_ok = (head_dim % 8 == 0) && aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
+  if (pg.table) {
+    MKQ_REQUIRE(pg.block_size > 0 && pg.block_size % 16 == 0, "%s: block_size %d must be a positive multiple of 16",
+                fn, pg.block_size);
+    MKQ_REQUIRE(pg.num_blocks > 0 && pg.max_blocks > 0, "%s: num_blocks and max_blocks must be positive", fn);
+    MKQ_REQUIRE(int64_t(pg.max_blocks) * pg.block_size >= seq_len, "%s: max_blocks * block_size < seq_len", fn);
+    if (!fast_ok || (dtype != MKQ_DTYPE_BF16 && dtype != MKQ_DTYPE_F16))
+      return set_error(MKQ_ERR_UNSUPPORTED,
+                       "%s: the paged layout needs bf16/f16, head_dim %% 8 == 0 and 16-byte aligned tensors", fn);
+  }
   if (ap.k_new) {
     MKQ_REQUIRE(ap.v_new, "%s: null tensor pointer", fn);
     MKQ_REQUIRE(ap.cap >= seq_len, "%s: capacity %d is below seq_len %d", fn, ap.cap, seq_len);
@@ -760,12 +847,12 @@ int attention_entry(const char* fn, int dtype, const void* q, const void* k_cach
   switch (dtype) {
     case MKQ_DTYPE_BF16:
       return fast_ok ? launch_fast_d<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                             scale, rope_cs, rot, ap, ws, s)
+                                             scale, rope_cs, rot, ap, pg, ws, s)
                      : launch_generic<bf16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                               scale, ws, s);
     case MKQ_DTYPE_F16:
       return fast_ok ? launch_fast_d<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
-                                            scale, rope_cs, rot, ap, ws, s)
+                                            scale, rope_cs, rot, ap, pg, ws, s)
                      : launch_generic<f16_t>(q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len,
                                              scale, ws, s);
     case MKQ_DTYPE_F32:
@@ -782,7 +869,7 @@ extern "C" int mkq_full_attention_decode(int dtype, const void* q, const void* k
                                          void* out, int batch, int q_heads, int kv_heads, int head_dim, int seq_len,
                                          float scale, void* workspace, size_t workspace_bytes, void* stream) {
   return attention_entry("full_attention_decode", dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads,
-                         head_dim, seq_len, scale, nullptr, 0, Append{}, workspace, workspace_bytes, stream);
+                         head_dim, seq_len, scale, nullptr, 0, Append{}, Paged{}, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mkq_full_attention_decode_rope(int dtype, const void* q, const void* k_cache, const void* v_cache,
@@ -790,8 +877,8 @@ extern "C" int mkq_full_attention_decode_rope(int dtype, const void* q, const vo
                                               int seq_len, float scale, const float* cos_sin, int rotary_dim,
                                               void* workspace, size_t workspace_bytes, void* stream) {
   return attention_entry("full_attention_decode_rope", dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads,
-                         head_dim, seq_len, scale, cos_sin, rotary_dim, Append{}, workspace, workspace_bytes,
-                         stream);
+                         head_dim, seq_len, scale, cos_sin, rotary_dim, Append{}, Paged{}, workspace,
+                         workspace_bytes, stream);
 }
 
 extern "C" int mkq_full_attention_decode_append(int dtype, const void* q, const void* k_new, const void* v_new,
@@ -809,5 +896,24 @@ extern "C" int mkq_full_attention_decode_append(int dtype, const void* q, const 
   ap.v_new = v_new;
   ap.cap = capacity;
   return attention_entry(fn, dtype, q, k_cache, v_cache, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
-                         cos_sin, cos_sin ? rotary_dim : 0, ap, workspace, workspace_bytes, stream);
+                         cos_sin, cos_sin ? rotary_dim : 0, ap, Paged{}, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mkq_full_attention_decode_paged(int dtype, const void* q, const void* k_blocks, const void* v_blocks,
+                                               const int* block_table, void* out, int batch, int q_heads,
+                                               int kv_heads, int head_dim, int seq_len, int block_size,
+                                               int max_blocks, int num_blocks, float scale, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+  const char* fn = "full_attention_decode_paged";
+  if (!block_table) {
+    clear_error();
+    return set_error(MKQ_ERR_INVALID, "%s: null tensor pointer", fn);
+  }
+  Paged pg;
+  pg.table = block_table;
+  pg.block_size = block_size;
+  pg.max_blocks = max_blocks;
+  pg.num_blocks = num_blocks;
+  return attention_entry(fn, dtype, q, k_blocks, v_blocks, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
+                         nullptr, 0, Append{}, pg, workspace, workspace_bytes, stream);
 }

@@ -298,6 +298,43 @@ torch::Tensor full_attention_decode_append(torch::Tensor q, torch::Tensor k_new,
   return out;
 }
 
+// q [B, Hq, D]; k_blocks/v_blocks [num_blocks, block_size, Hkv, D];
+// block_table [B, max_blocks] int32; attends over the first seq_len tokens.
+torch::Tensor full_attention_decode_paged(torch::Tensor q, torch::Tensor k_blocks, torch::Tensor v_blocks,
+                                          torch::Tensor block_table, int64_t seq_len, double scale) {
+  MK_CHECK_INPUT(q);
+  MK_CHECK_INPUT(k_blocks);
+  MK_CHECK_INPUT(v_blocks);
+  MK_CHECK_INPUT(block_table);
+  TORCH_CHECK(q.dim() == 3, "q must be [batch, query_heads, head_dim]");
+  TORCH_CHECK(k_blocks.dim() == 4, "k_blocks must be [num_blocks, block_size, kv_heads, head_dim]");
+  TORCH_CHECK(v_blocks.sizes() == k_blocks.sizes(), "v_blocks shape must match k_blocks");
+  TORCH_CHECK(q.scalar_type() == k_blocks.scalar_type() && q.scalar_type() == v_blocks.scalar_type(),
+              "q and the block pools dtype mismatch");
+  TORCH_CHECK(block_table.scalar_type() == torch::kInt32 && block_table.dim() == 2 &&
+                  block_table.size(0) == q.size(0),
+              "block_table must be int32 [batch, max_blocks]");
+  const int batch = static_cast<int>(q.size(0));
+  const int query_heads = static_cast<int>(q.size(1));
+  const int head_dim = static_cast<int>(q.size(2));
+  const int kv_heads = static_cast<int>(k_blocks.size(2));
+  TORCH_CHECK(k_blocks.size(3) == head_dim, "head_dim mismatch");
+  TORCH_CHECK(kv_heads > 0 && query_heads % kv_heads == 0, "query_heads must be divisible by kv_heads");
+  TORCH_CHECK(seq_len > 0, "seq_len must be positive");
+  const int seq = static_cast<int>(seq_len);
+  c10::DeviceGuard guard(q.device());
+  auto out = torch::empty_like(q);
+  auto ws = workspace_for(Ws::kAttention, q,
+                          mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq));
+  const int rc = mkq_full_attention_decode_paged(
+      to_mkq_dtype(q), q.data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(), block_table.data_ptr<int>(),
+      out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq, static_cast<int>(k_blocks.size(1)),
+      static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)), static_cast<float>(scale),
+      ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream());
+  check_status(rc, "full_attention_decode_paged");
+  return out;
+}
+
 std::tuple<torch::Tensor, torch::Tensor> linear_attention_decode(torch::Tensor q, torch::Tensor k, torch::Tensor v,
                                                                  torch::Tensor state, double decay) {
   // Checks and messages as in linear_attention_decode.cu:52-69.
@@ -502,6 +539,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "KV append fused into the split-K GQA flash-decode (HIP)", pybind11::arg("q"), pybind11::arg("k_new"),
         pybind11::arg("v_new"), pybind11::arg("k_cache"), pybind11::arg("v_cache"), pybind11::arg("seq_len"),
         pybind11::arg("scale"), pybind11::arg("cos_sin") = pybind11::none(), pybind11::arg("rotary_dim") = 0);
+  m.def("full_attention_decode_paged", &full_attention_decode_paged,
+        "Split-K GQA flash-decode over a paged KV pool (HIP)", pybind11::arg("q"), pybind11::arg("k_blocks"),
+        pybind11::arg("v_blocks"), pybind11::arg("block_table"), pybind11::arg("seq_len"), pybind11::arg("scale"));
   m.def("linear_attention_decode", &linear_attention_decode, "Recurrent linear-attention decode (HIP)");
   m.def("gated_delta_decode", &gated_delta_decode, "Gated delta rule decode (HIP)", pybind11::arg("q"),
         pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("state"), pybind11::arg("g"), pybind11::arg("beta"),

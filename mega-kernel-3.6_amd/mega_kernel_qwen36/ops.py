@@ -97,6 +97,12 @@ class FullAttentionInputs:
     k_new: Optional[torch.Tensor] = None
     v_new: Optional[torch.Tensor] = None
     cache_seqlen: Optional[int] = None
+    # Paged KV (no counterpart in the reference): with a block_table
+    # [batch, max_blocks] (int32), k_cache/v_cache are block pools
+    # [num_blocks, block_size, kv_heads, head_dim] and seq_len tokens are read
+    # (default max_blocks * block_size).
+    block_table: Optional[torch.Tensor] = None
+    seq_len: Optional[int] = None
 
 
 @dataclass(frozen=True)
@@ -362,6 +368,46 @@ def _attention_append(inputs: FullAttentionInputs) -> torch.Tensor:
                                                      cache_seqlen=None))
 
 
+def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
+    """Attention over a paged KV pool: token t of batch row b is row
+    t % block_size of block block_table[b, t // block_size].  The kernel reads
+    the blocks in place (bf16/f16, head_dim % 8 == 0, block_size % 16 == 0);
+    other cases gather the rows into a contiguous cache first.  RoPE and the
+    KV append are not combined with the paged layout."""
+    if inputs.k_new is not None or inputs.v_new is not None:
+        raise ValueError("k_new/v_new are not supported with a block_table")
+    if inputs.cos is not None or inputs.sin is not None:
+        raise ValueError("cos/sin are not supported with a block_table")
+    kb, vb, table = inputs.k_cache, inputs.v_cache, inputs.block_table
+    if kb.dim() != 4 or vb.shape != kb.shape:
+        raise ValueError("k_cache and v_cache must be [num_blocks, block_size, kv_heads, head_dim] with a block_table")
+    q = inputs.q
+    nblocks, bs, hkv, d = kb.shape
+    if table.dim() != 2 or table.shape[0] != q.shape[0]:
+        raise ValueError("block_table must be [batch, max_blocks]")
+    seq = int(inputs.seq_len) if inputs.seq_len is not None else table.shape[1] * bs
+    if not 0 < seq <= table.shape[1] * bs:
+        raise ValueError("seq_len must be in [1, max_blocks * block_size]")
+    if q.shape[1] % hkv != 0:
+        raise ValueError("query_heads must be divisible by kv_heads")
+    _require_extension("full_attention_decode", q, kb, vb, table)
+    scale = inputs.scale if inputs.scale is not None else 1.0 / math.sqrt(d)
+    if kb.dtype in (torch.bfloat16, torch.float16) and d % 8 == 0 and bs % 16 == 0 and q.dtype == kb.dtype:
+        return _C.full_attention_decode_paged(q.contiguous(), kb.contiguous(), vb.contiguous(),
+                                              table.to(torch.int32).contiguous(), seq, float(scale))
+    # Gather the blocks that hold the seq_len tokens; ids outside the pool
+    # read as zeros, as in the kernel (never an out-of-range index).
+    idx = table[:, : (seq + bs - 1) // bs].long()
+    valid = ((idx >= 0) & (idx < nblocks))[..., None, None, None]
+    safe = idx.clamp(0, nblocks - 1)
+    k = torch.where(valid, kb[safe], torch.zeros((), dtype=kb.dtype, device=kb.device))
+    v = torch.where(valid, vb[safe], torch.zeros((), dtype=vb.dtype, device=vb.device))
+    k = k.reshape(q.shape[0], -1, hkv, d)[:, :seq]
+    v = v.reshape(q.shape[0], -1, hkv, d)[:, :seq]
+    return full_attention_decode(dataclasses.replace(inputs, k_cache=k, v_cache=v, block_table=None,
+                                                     seq_len=None, scale=scale))
+
+
 def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:
     """One-token GQA attention over a contiguous KV cache (split-K flash-decode, HIP).
 
@@ -371,6 +417,8 @@ def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:
     otherwise both are rotated first, as the reference does.  Device-resident
     cos/sin avoid a host-to-device copy per call.  With k_new/v_new the new
     token is appended to the caches first (see _attention_append)."""
+    if inputs.block_table is not None:
+        return _attention_paged(inputs)
     if inputs.k_new is not None or inputs.v_new is not None:
         return _attention_append(inputs)
     cs = _rope_in_kernel(inputs)

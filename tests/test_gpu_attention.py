@@ -326,3 +326,80 @@ def test_attention_append_fallback_writes_then_attends(d, dtype, rot):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.equal(k_cache, k_ref) and torch.equal(v_cache, v_ref)
+
+
+def _paged_case(inp, bs, seed, bad_block=None):
+    """Scatter a contiguous cache into a shuffled block pool (padding rows and
+    unused blocks hold garbage); returns (pool_k, pool_v, table, expected
+    contiguous k/v).  With bad_block=(row, j) that table entry is set outside
+    the pool, and the expected cache has zeros there."""
+    b, t, hkv, d = inp.k_cache.shape
+    nb = (t + bs - 1) // bs
+    g = torch.Generator().manual_seed(seed)
+    num_blocks = b * nb + 5
+    perm = torch.randperm(num_blocks, generator=g)[: b * nb].reshape(b, nb)
+    pad = nb * bs - t
+    pool_k = torch.randn(num_blocks, bs, hkv, d, generator=g).to("cuda", inp.k_cache.dtype)
+    pool_v = torch.randn(num_blocks, bs, hkv, d, generator=g).to("cuda", inp.k_cache.dtype)
+    garbage = torch.randn(b, pad, hkv, d, generator=g).to("cuda", inp.k_cache.dtype)
+    kp = torch.cat([inp.k_cache, garbage], 1).reshape(b, nb, bs, hkv, d)
+    vp = torch.cat([inp.v_cache, garbage], 1).reshape(b, nb, bs, hkv, d)
+    for r in range(b):
+        pool_k[perm[r].cuda()] = kp[r]
+        pool_v[perm[r].cuda()] = vp[r]
+    table = torch.full((b, nb + 1), 1 << 30, dtype=torch.int32)
+    table[:, :nb] = perm.to(torch.int32)
+    k_want, v_want = inp.k_cache.clone(), inp.v_cache.clone()
+    if bad_block is not None:
+        r, j = bad_block
+        table[r, j] = -7
+        k_want[r, j * bs:(j + 1) * bs] = 0
+        v_want[r, j * bs:(j + 1) * bs] = 0
+    return pool_k, pool_v, table.cuda(), k_want, v_want
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t,bs,dtype", [
+    (1, 24, 4, 256, 32768, 16, torch.bfloat16),   # config 4 in 16-token blocks
+    (1, 24, 4, 256, 4096, 256, torch.bfloat16),
+    (3, 8, 2, 128, 3001, 64, torch.float16),      # ragged last block
+    (2, 40, 2, 128, 700, 32, torch.bfloat16),     # group 20: two head groups
+    (1, 4, 4, 64, 1, 16, torch.bfloat16),         # one token
+])
+def test_attention_paged_equals_contiguous(b, hq, hkv, d, t, bs, dtype):
+    """The paged kernel over a shuffled block pool is bit-identical to the
+    contiguous kernel over the same tokens; rows past seq_len and unused
+    blocks (garbage) are never read."""
+    inp = make_attention(batch=b, q_heads=hq, kv_heads=hkv, head_dim=d, seq_len=t, seed=600 + t, dtype=dtype)
+    pk, pv, table, _, _ = _paged_case(inp, bs, 601 + t)
+    got = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk, pv, scale=inp.scale, block_table=table,
+                                                          seq_len=t))
+    want = mk.full_attention_decode(inp)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    if t <= 4096:
+        assert_close_out(got, _ref(inp))
+
+
+def test_attention_paged_block_outside_pool_reads_zeros():
+    """A table entry outside [0, num_blocks) reads as zeros instead of
+    faulting: the result equals the contiguous kernel with those rows zeroed."""
+    inp = make_attention(batch=2, q_heads=8, kv_heads=2, head_dim=128, seq_len=1000, seed=610)
+    pk, pv, table, kz, vz = _paged_case(inp, 64, 611, bad_block=(1, 3))
+    got = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk, pv, scale=inp.scale, block_table=table,
+                                                          seq_len=1000))
+    want = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, kz, vz, scale=inp.scale))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("d,bs,dtype", [(128, 8, torch.bfloat16), (20, 16, torch.bfloat16), (64, 16, torch.float32)])
+def test_attention_paged_fallback_gathers(d, bs, dtype):
+    """Block sizes or head dims the kernel does not read in place are gathered
+    into a contiguous cache first; the result equals the contiguous path."""
+    inp = make_attention(batch=2, q_heads=4, kv_heads=2, head_dim=d, seq_len=77, seed=620 + d, dtype=dtype)
+    pk, pv, table, _, _ = _paged_case(inp, bs, 621)
+    got = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk, pv, scale=inp.scale, block_table=table,
+                                                          seq_len=77))
+    want = mk.full_attention_decode(inp)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

@@ -227,3 +227,26 @@ def test_configs_match_published_dims():
     assert [mk.qwen36_layer_type(i) for i in range(8)] == ["linear_attention"] * 3 + ["full_attention"] + \
         ["linear_attention"] * 3 + ["full_attention"]
     assert c.rotary_dim == 64
+
+
+def test_paged_entry_validates_on_the_host_without_gpu():
+    """mkq_full_attention_decode_paged checks its layout before any launch:
+    a null table, a block size that is not a multiple of 16 or too few blocks
+    for seq_len (INVALID), FP32 (UNSUPPORTED).  Host buffers, never touched."""
+    lib = _lib.load_library()
+    b, hq, hkv, d, t = 1, 4, 2, 64, 40
+    nbytes = lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t)
+    raw = ctypes.create_string_buffer(nbytes + 512)
+    ws = (ctypes.addressof(raw) + 255) // 256 * 256
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    call = lib.mkq_full_attention_decode_paged
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, None, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, b, hq, hkv, d, t, 24, 3, 8, 1.0, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert b"block_size" in lib.mkq_last_error()
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, b, hq, hkv, d, t, 16, 2, 8, 1.0, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert call(_lib.MKQ_DTYPE_F32, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, ws, nbytes,
+                None) == _lib.MKQ_ERR_UNSUPPORTED
