@@ -288,6 +288,23 @@ def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
                 log(f"attention T={t} with KV append ({'in the kernel' if 'torch' not in name else 'row written by torch first'}): "
                     f"{r['median_us']:.2f} us cold in stream, {r['warm_median_us']:.2f} us warm")
             del kc, vc
+            # Paged KV: the same cache scattered over a shuffled pool of
+            # 16- and 256-token blocks, read in place through a block table.
+            for bs in (16, 256):
+                nb = t // bs
+                perm = torch.randperm(nb + 8, generator=torch.Generator().manual_seed(bs))[:nb]
+                pk = torch.empty(nb + 8, bs, 4, 256, dtype=inp.k_cache.dtype, device="cuda")
+                pv = torch.empty_like(pk)
+                pk[perm.cuda()] = inp.k_cache.reshape(nb, bs, 4, 256)
+                pv[perm.cuda()] = inp.v_cache.reshape(nb, bs, 4, 256)
+                paged = mk.FullAttentionInputs(q=inp.q, k_cache=pk, v_cache=pv,
+                                               block_table=perm.to(torch.int32)[None].cuda(), seq_len=t)
+                r = measure(timer, lambda: mk.full_attention_decode(paged), steps, warmup,  # noqa: B023
+                            attn_bytes(1, 24, 4, 256, t))
+                out[f"attn_paged{bs}_t32768"] = r
+                log(f"attention T={t} paged ({bs}-token blocks): {r['median_us']:.2f} us cold in stream, "
+                    f"{r['warm_median_us']:.2f} us warm")
+                del pk, pv
         del inp
         torch.cuda.empty_cache()
     return out
