@@ -348,9 +348,19 @@ def bench_linear(mk, inputs, timer, steps, warmup, batches):
             o, _ = mk.linear_attention_decode(dataclasses.replace(inp, q=q, k=k, v=v, qk_l2norm=True))
             return mk.gated_rms_norm(o, zg, nw)
 
-        r = measure(timer, step, steps, warmup, linear_bytes(b, 16, 32, 128, 128) + 8192 * 4 * 2 + b * 8192 * 3 * 4)
+        step_bytes = linear_bytes(b, 16, 32, 128, 128) + 8192 * 4 * 2 + b * 8192 * 3 * 4
+        r = measure(timer, step, steps, warmup, step_bytes)
+        out[f"linear_step_composed_b{b}"] = r
+        log(f"linear step b={b} composed in Python (conv update, recurrence with q/k norm, gated norm): "
+            f"{r['median_us']:.2f} us cold in stream, {r['warm_median_us']:.2f} us warm")
+        st = inp.state.clone()
+
+        def one_call(b=b, st=st, conv_w=conv_w, conv_st=conv_st, xin=xin, zg=zg, nw=nw, inp=inp):
+            return mk.linear_attention_step(xin, conv_st, conv_w, st, inp.g, inp.beta, zg, nw, k_heads=16)
+
+        r = measure(timer, one_call, steps, warmup, step_bytes)
         out[f"linear_step_b{b}"] = r
-        log(f"linear step b={b} (conv update + recurrence with q/k norm + gated norm): "
+        log(f"linear step b={b} in one call (mkq_linear_attention_step): "
             f"{r['median_us']:.2f} us cold in stream, {r['warm_median_us']:.2f} us warm")
     return out
 

@@ -218,6 +218,29 @@ int mkq_causal_conv1d_update(int dtype, const void* x, void* conv_state, const v
 int mkq_gated_rms_norm(int dtype, const void* x, const void* gate, const void* weight, void* out,
                        int rows, int dim, float eps, void* stream);
 
+/* One Qwen3.6 linear-attention step around and through the recurrence, in
+ * three launches on `stream` with no host work between them:
+ *   mixed = silu(conv(x_mixed))   (mkq_causal_conv1d_update, conv_state in place)
+ *   q, k, v = the [k_heads*key_dim | k_heads*key_dim | v_heads*value_dim]
+ *             parts of mixed, read in place
+ *   o = gated delta rule with q/k L2 norm and q_scale (state updated in place)
+ *   out = mkq_gated_rms_norm(o, z, norm_weight, eps)
+ * x_mixed [batch, C] with C = 2*k_heads*key_dim + v_heads*value_dim;
+ * conv_state [batch, C, conv_state_len]; conv_weight [C, conv_state_len+1];
+ * conv_bias [C] or NULL; state [batch, v_heads, key_dim, value_dim] FP32;
+ * g, beta [batch, v_heads] FP32; z, out [batch, v_heads, value_dim];
+ * norm_weight [value_dim].  The workspace (mixed and o) is sized by
+ * mkq_linear_attention_step_workspace_bytes and 256-byte aligned; it holds
+ * no state between calls.  No counterpart in the reference. */
+size_t mkq_linear_attention_step_workspace_bytes(int dtype, int batch, int k_heads, int v_heads,
+                                                 int key_dim, int value_dim);
+int mkq_linear_attention_step(int dtype, const void* x_mixed, void* conv_state, const void* conv_weight,
+                              const void* conv_bias, int conv_state_len, float* state, const float* g,
+                              const float* beta, const void* z, const void* norm_weight, void* out,
+                              int batch, int k_heads, int v_heads, int key_dim, int value_dim,
+                              float q_scale, float eps, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* ------------------------------------------------------------------------
  * Plain GEMV used for the optional attention output projections in
  * decode_layer: y[b, n] = sum_k w[n, k] * x[b, k] (+ residual[b, n]).

@@ -32,7 +32,7 @@ template <typename T, bool GATED>
 __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* state,
     const float* __restrict__ g, const float* __restrict__ beta, T* __restrict__ out, float* new_state, int hk,
-    int hv, int dk, int dv, float decay, int qk_norm, float q_scale) {
+    int hv, int dk, int dv, float decay, int qk_norm, float q_scale, int qk_bs, int v_bs) {
   static_assert(kMaxKeyDim == kThreads, "one staged q/k element per thread");
   __shared__ float qs[kMaxKeyDim];
   __shared__ float ks[kMaxKeyDim];
@@ -59,10 +59,10 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
   // in flight while q/k are staged (and normalised).
   const int ti = threadIdx.x;  // staged q/k element, zero past dk
   const bool kin = ti < dk;
-  const size_t qo = (size_t(b) * hk + qh) * dk + (kin ? ti : 0);
+  const size_t qo = size_t(b) * qk_bs + size_t(qh) * dk + (kin ? ti : 0);  // qk_bs: batch stride
   float qv = to_f(q[qo]);
   float kv = to_f(k[qo]);
-  const float vraw = to_f(v[(size_t(b) * hv + vh) * dv + (col_ok ? j : 0)]);
+  const float vraw = to_f(v[size_t(b) * v_bs + size_t(vh) * dv + (col_ok ? j : 0)]);
   float d = decay, bt = 1.0f;
   if constexpr (GATED) {
     d = expf(g[size_t(b) * hv + vh]);
@@ -141,11 +141,11 @@ __global__ __launch_bounds__(kThreads) void linear_attention_kernel(
 template <typename T, bool GATED>
 int launch(const void* q, const void* k, const void* v, const float* state, const float* g, const float* beta,
            void* out, float* new_state, int batch, int hk, int hv, int dk, int dv, float decay, int qk_norm,
-           float q_scale, hipStream_t stream) {
+           float q_scale, int qk_bs, int v_bs, hipStream_t stream) {
   dim3 grid((dv + kWave - 1) / kWave, hv, batch);
   linear_attention_kernel<T, GATED><<<grid, kThreads, 0, stream>>>(
       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), state, g, beta,
-      static_cast<T*>(out), new_state, hk, hv, dk, dv, decay, qk_norm, q_scale);
+      static_cast<T*>(out), new_state, hk, hv, dk, dv, decay, qk_norm, q_scale, qk_bs, v_bs);
   MKQ_LAUNCH_CHECK("linear_attention_kernel");
   return MKQ_OK;
 }
@@ -153,18 +153,20 @@ int launch(const void* q, const void* k, const void* v, const float* state, cons
 template <bool GATED>
 int dispatch(int dtype, const void* q, const void* k, const void* v, const float* state, const float* g,
              const float* beta, void* out, float* new_state, int batch, int hk, int hv, int dk, int dv, float decay,
-             int qk_norm, float q_scale, void* stream) {
+             int qk_norm, float q_scale, void* stream, int qk_bs = 0, int v_bs = 0) {
+  if (qk_bs == 0) qk_bs = hk * dk;  // contiguous [B, H, D] by default
+  if (v_bs == 0) v_bs = hv * dv;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case MKQ_DTYPE_BF16:
       return launch<bf16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, qk_norm,
-                                   q_scale, s);
+                                   q_scale, qk_bs, v_bs, s);
     case MKQ_DTYPE_F16:
       return launch<f16_t, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, qk_norm,
-                                  q_scale, s);
+                                  q_scale, qk_bs, v_bs, s);
     case MKQ_DTYPE_F32:
       return launch<float, GATED>(q, k, v, state, g, beta, out, new_state, batch, hk, hv, dk, dv, decay, qk_norm,
-                                  q_scale, s);
+                                  q_scale, qk_bs, v_bs, s);
     default:
       return set_error(MKQ_ERR_INVALID, "linear attention: unknown dtype %d", dtype);
   }
@@ -216,4 +218,59 @@ extern "C" int mkq_gated_delta_decode_qknorm(int dtype, const void* q, const voi
                                              int value_dim, float q_scale, void* stream) {
   return gated_entry("gated_delta_decode_qknorm", dtype, q, k, v, state, g, beta, out, new_state, batch, k_heads,
                      v_heads, key_dim, value_dim, 1, q_scale, stream);
+}
+
+namespace {
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+size_t elt_size(int dtype) {
+  return dtype == MKQ_DTYPE_F32 ? 4 : (dtype == MKQ_DTYPE_BF16 || dtype == MKQ_DTYPE_F16) ? 2 : 0;
+}
+
+}  // namespace
+
+extern "C" size_t mkq_linear_attention_step_workspace_bytes(int dtype, int batch, int k_heads, int v_heads,
+                                                            int key_dim, int value_dim) {
+  const size_t elt = elt_size(dtype);
+  if (elt == 0 || batch <= 0 || k_heads <= 0 || v_heads <= 0 || key_dim <= 0 || value_dim <= 0) return 0;
+  const size_t channels = 2 * size_t(k_heads) * key_dim + size_t(v_heads) * value_dim;
+  return align256(size_t(batch) * channels * elt) + align256(size_t(batch) * v_heads * value_dim * elt);
+}
+
+// The three launches of one Qwen3.6 linear-attention step on one stream: the
+// conv update writes the mixed q/k/v row into the workspace, the recurrence
+// reads q, k and v from it in place (batch stride = the channel count) and
+// updates the state in place, and the gated norm writes `out`.
+extern "C" int mkq_linear_attention_step(int dtype, const void* x_mixed, void* conv_state, const void* conv_weight,
+                                         const void* conv_bias, int conv_state_len, float* state, const float* g,
+                                         const float* beta, const void* z, const void* norm_weight, void* out,
+                                         int batch, int k_heads, int v_heads, int key_dim, int value_dim,
+                                         float q_scale, float eps, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  clear_error();
+  const char* fn = "linear_attention_step";
+  MKQ_REQUIRE(batch > 0 && k_heads > 0 && v_heads > 0 && key_dim > 0 && value_dim > 0 && conv_state_len > 0,
+              "%s: sizes must be positive", fn);
+  MKQ_REQUIRE(v_heads % k_heads == 0, "%s: v_heads must be a multiple of k_heads", fn);
+  MKQ_REQUIRE(x_mixed && conv_state && conv_weight && state && g && beta && z && norm_weight && out,
+              "%s: null tensor pointer", fn);
+  if (key_dim > kMaxKeyDim) return set_error(MKQ_ERR_UNSUPPORTED, "%s: key_dim %d > %d", fn, key_dim, kMaxKeyDim);
+  MKQ_REQUIRE(batch <= 65535 && v_heads <= 65535, "%s: batch/heads too large", fn);
+  const size_t need = mkq_linear_attention_step_workspace_bytes(dtype, batch, k_heads, v_heads, key_dim, value_dim);
+  MKQ_REQUIRE(need > 0, "%s: unknown dtype %d", fn, dtype);
+  MKQ_REQUIRE(workspace && workspace_bytes >= need, "%s: workspace too small", fn);
+  MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "%s: workspace must be 256-byte aligned", fn);
+  const size_t elt = elt_size(dtype);
+  const int channels = 2 * k_heads * key_dim + v_heads * value_dim;
+  unsigned char* mixed = static_cast<unsigned char*>(workspace);
+  unsigned char* o = mixed + align256(size_t(batch) * channels * elt);
+  int rc = mkq_causal_conv1d_update(dtype, x_mixed, conv_state, conv_weight, conv_bias, mixed, batch, channels,
+                                    conv_state_len, 1, stream);
+  if (rc != MKQ_OK) return rc;
+  const size_t kd = size_t(k_heads) * key_dim * elt;
+  rc = dispatch<true>(dtype, mixed, mixed + kd, mixed + 2 * kd, state, g, beta, o, state, batch, k_heads, v_heads,
+                      key_dim, value_dim, 1.0f, 1, q_scale, stream, channels, channels);
+  if (rc != MKQ_OK) return rc;
+  return mkq_gated_rms_norm(dtype, o, z, norm_weight, out, batch * v_heads, value_dim, eps, stream);
 }

@@ -50,7 +50,7 @@ hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); 
 // next call of the same entry point, so the buffer is cleared only when it is
 // first allocated (or grown); entry points do not share one, since another
 // entry point's scratch data would overwrite that state.
-enum class Ws { kMoe, kDense, kAttention };
+enum class Ws { kMoe, kDense, kAttention, kLinearStep };
 torch::Tensor workspace_for(Ws op, const torch::Tensor& like, size_t bytes) {
   static std::map<std::tuple<int, int, hipStream_t>, torch::Tensor> cache;
   const auto key = std::make_tuple(static_cast<int>(op), static_cast<int>(like.get_device()), current_stream());
@@ -480,6 +480,64 @@ torch::Tensor gated_rms_norm(torch::Tensor x, torch::Tensor gate, torch::Tensor 
   return out;
 }
 
+// One Qwen3.6 linear-attention step: conv update (conv_state in place), the
+// gated delta rule with q/k L2 norm (state in place), gated RMS norm.
+torch::Tensor linear_attention_step(torch::Tensor x_mixed, torch::Tensor conv_state, torch::Tensor conv_weight,
+                                    c10::optional<torch::Tensor> conv_bias, torch::Tensor state, torch::Tensor g,
+                                    torch::Tensor beta, torch::Tensor z, torch::Tensor norm_weight, int64_t k_heads,
+                                    double q_scale, double eps) {
+  MK_CHECK_INPUT(x_mixed);
+  MK_CHECK_INPUT(conv_state);
+  MK_CHECK_INPUT(conv_weight);
+  MK_CHECK_INPUT(state);
+  MK_CHECK_INPUT(g);
+  MK_CHECK_INPUT(beta);
+  MK_CHECK_INPUT(z);
+  MK_CHECK_INPUT(norm_weight);
+  TORCH_CHECK(x_mixed.dim() == 2, "x_mixed must be [batch, channels]");
+  TORCH_CHECK(state.dim() == 4 && state.scalar_type() == torch::kFloat32,
+              "state must be float32 [batch, v_heads, key_dim, value_dim]");
+  TORCH_CHECK(z.dim() == 3, "z must be [batch, v_heads, value_dim]");
+  const int64_t batch = x_mixed.size(0), c = x_mixed.size(1);
+  const int64_t hv = state.size(1), dk = state.size(2), dv = state.size(3);
+  TORCH_CHECK(state.size(0) == batch && z.size(0) == batch && z.size(1) == hv && z.size(2) == dv,
+              "state/z batch or head mismatch");
+  TORCH_CHECK(k_heads > 0 && c == 2 * k_heads * dk + hv * dv, "channels must be 2*k_heads*key_dim + v_heads*value_dim");
+  TORCH_CHECK(conv_state.dim() == 3 && conv_state.size(0) == batch && conv_state.size(1) == c,
+              "conv_state must be [batch, channels, state_len]");
+  TORCH_CHECK(conv_weight.dim() == 2 && conv_weight.size(0) == c && conv_weight.size(1) == conv_state.size(2) + 1,
+              "conv_weight must be [channels, state_len + 1]");
+  TORCH_CHECK(norm_weight.numel() == dv, "norm_weight must be [value_dim]");
+  TORCH_CHECK(g.numel() == batch * hv && beta.numel() == batch * hv && g.scalar_type() == torch::kFloat32 &&
+                  beta.scalar_type() == torch::kFloat32,
+              "g and beta must be float32 [batch, v_heads]");
+  const auto dt = x_mixed.scalar_type();
+  TORCH_CHECK(conv_state.scalar_type() == dt && conv_weight.scalar_type() == dt && z.scalar_type() == dt &&
+                  norm_weight.scalar_type() == dt,
+              "x_mixed, conv_state, conv_weight, z and norm_weight must share a dtype");
+  const void* bias = nullptr;
+  if (conv_bias.has_value()) {
+    MK_CHECK_INPUT((*conv_bias));
+    TORCH_CHECK(conv_bias->numel() == c && conv_bias->scalar_type() == dt, "conv_bias must be [channels]");
+    bias = conv_bias->data_ptr();
+  }
+  c10::DeviceGuard guard(x_mixed.device());
+  auto out = torch::empty_like(z);
+  const int dtype = to_mkq_dtype(x_mixed);
+  const size_t need = mkq_linear_attention_step_workspace_bytes(dtype, static_cast<int>(batch), static_cast<int>(k_heads),
+                                                                static_cast<int>(hv), static_cast<int>(dk),
+                                                                static_cast<int>(dv));
+  auto ws = workspace_for(Ws::kLinearStep, x_mixed, need);
+  const int rc = mkq_linear_attention_step(
+      dtype, x_mixed.data_ptr(), conv_state.data_ptr(), conv_weight.data_ptr(), bias,
+      static_cast<int>(conv_state.size(2)), state.data_ptr<float>(), g.data_ptr<float>(), beta.data_ptr<float>(),
+      z.data_ptr(), norm_weight.data_ptr(), out.data_ptr(), static_cast<int>(batch), static_cast<int>(k_heads),
+      static_cast<int>(hv), static_cast<int>(dk), static_cast<int>(dv), static_cast<float>(q_scale),
+      static_cast<float>(eps), ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream());
+  check_status(rc, "linear_attention_step");
+  return out;
+}
+
 torch::Tensor gemv(torch::Tensor x, torch::Tensor w, c10::optional<torch::Tensor> residual) {
   MK_CHECK_INPUT(x);
   MK_CHECK_INPUT(w);
@@ -554,6 +612,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("bias") = pybind11::none(), pybind11::arg("silu_activation") = true);
   m.def("gated_rms_norm", &gated_rms_norm, "Gated RMS norm, norm before gate (HIP)", pybind11::arg("x"),
         pybind11::arg("gate"), pybind11::arg("weight"), pybind11::arg("eps") = 1e-6);
+  m.def("linear_attention_step", &linear_attention_step,
+        "Qwen3.6 linear-attention step: conv update, gated delta rule with q/k norm, gated norm (HIP)",
+        pybind11::arg("x_mixed"), pybind11::arg("conv_state"), pybind11::arg("conv_weight"),
+        pybind11::arg("conv_bias"), pybind11::arg("state"), pybind11::arg("g"), pybind11::arg("beta"),
+        pybind11::arg("z"), pybind11::arg("norm_weight"), pybind11::arg("k_heads"), pybind11::arg("q_scale"),
+        pybind11::arg("eps"));
   m.def("gemv", &gemv, "y = x w^T (+ residual) (HIP)", pybind11::arg("x"), pybind11::arg("w"),
         pybind11::arg("residual") = pybind11::none());
   m.def("gemv_add", &gemv_add, "(y, residual + y) with y = x w^T (HIP)", pybind11::arg("x"), pybind11::arg("w"),

@@ -27,6 +27,7 @@ from .ops import (
     full_attention_decode,
     gated_rms_norm,
     linear_attention_decode,
+    linear_attention_step,
     moe_decode,
 )
 from ._lib import library_path, load_library
@@ -48,6 +49,7 @@ __all__ = [
     "gated_rms_norm",
     "library_path",
     "linear_attention_decode",
+    "linear_attention_step",
     "load_library",
     "moe_decode",
     "qwen36_27b_config",

@@ -54,6 +54,9 @@ SIGNATURES = {
         _i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "mkq_causal_conv1d_update": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "mkq_gated_rms_norm": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
+    "mkq_linear_attention_step_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "mkq_linear_attention_step": (_i, [_i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i,
+                                       _f, _f, _vp, _sz, _vp]),
     "mkq_gemv": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mkq_gemv_add": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }

@@ -472,6 +472,41 @@ def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, ep
     return _C.gated_rms_norm(x.contiguous(), gate.contiguous(), weight.contiguous(), float(eps))
 
 
+def linear_attention_step(
+    x_mixed: torch.Tensor,
+    conv_state: torch.Tensor,
+    conv_weight: torch.Tensor,
+    state: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    z: torch.Tensor,
+    norm_weight: torch.Tensor,
+    *,
+    k_heads: int,
+    conv_bias: Optional[torch.Tensor] = None,
+    q_scale: Optional[float] = None,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """One Qwen3.6 linear-attention decode step from the projected q/k/v row
+    to the gated-norm output, in three launches with no host work between
+    them: causal conv update of x_mixed [batch, 2*k_heads*Dk + Hv*Dv]
+    (conv_state updated in place), the gated delta rule with q/k L2 norm
+    reading q, k and v from the conv output in place (state [batch, Hv, Dk,
+    Dv] FP32 updated in place), and the gated RMS norm with z [batch, Hv, Dv].
+    Returns out [batch, Hv, Dv].  No counterpart in the reference."""
+    _require_extension("linear_attention_step", x_mixed, conv_state, conv_weight, state, g, beta, z, norm_weight)
+    for name, t in (("conv_state", conv_state), ("state", state)):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous: it is updated in place")
+    dk = state.shape[2]
+    scale = q_scale if q_scale is not None else 1.0 / math.sqrt(dk)
+    w = conv_weight.reshape(conv_weight.shape[0], conv_weight.shape[-1]).contiguous()
+    return _C.linear_attention_step(x_mixed.contiguous(), conv_state, w,
+                                    None if conv_bias is None else conv_bias.contiguous(), state,
+                                    g.float().contiguous(), beta.float().contiguous(), z.contiguous(),
+                                    norm_weight.contiguous(), int(k_heads), float(scale), float(eps))
+
+
 def linear_attention_decode(inputs: LinearAttentionInputs) -> tuple[torch.Tensor, torch.Tensor]:
     """One recurrent step.  Returns ``(out, new_state)``; the input state is not modified.
 

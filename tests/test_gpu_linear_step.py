@@ -95,3 +95,62 @@ def test_gated_rms_norm_head_layout():
     torch.cuda.synchronize()
     ref = oracle.gated_rms_norm(np32(x).reshape(-1, 128), np32(z).reshape(-1, 128), np32(w))
     assert_close_out(out.reshape(-1, 128), ref)
+
+
+def _step_case(batch, hk, hv, dk, dv, dtype, seed):
+    c = 2 * hk * dk + hv * dv
+    g = torch.Generator().manual_seed(seed)
+
+    def r(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to("cuda", dtype)
+
+    x = r(batch, c)
+    conv_state = r(batch, c, 3)
+    conv_w = r(c, 4, scale=0.5)
+    state = (torch.randn(batch, hv, dk, dv, generator=g) * 0.1).cuda()
+    gg = -torch.nn.functional.softplus(torch.randn(batch, hv, generator=g)).cuda()
+    beta = torch.sigmoid(torch.randn(batch, hv, generator=g)).cuda()
+    z = r(batch, hv, dv)
+    nw = r(dv, scale=0.2) + 1.0
+    return x, conv_state, conv_w, state, gg, beta, z, nw
+
+
+@pytest.mark.parametrize("batch,hk,hv,dk,dv,dtype", [
+    (1, 16, 32, 128, 128, torch.bfloat16),   # Qwen3.6-35B-A3B linear attention
+    (8, 16, 32, 128, 128, torch.bfloat16),
+    (3, 2, 4, 64, 32, torch.float16),
+])
+def test_linear_attention_step_equals_composition(batch, hk, hv, dk, dv, dtype):
+    """The one-call step (q/k/v read from the conv output in place, states
+    updated in place) is bit-identical to composing the separate ops on
+    copies, and agrees with the oracle's chain of restatements."""
+    x, cs, cw, st, gg, beta, z, nw = _step_case(batch, hk, hv, dk, dv, dtype, 700 + batch)
+    cs2, st2 = cs.clone(), st.clone()
+    np_cs, np_st = np32(cs), np32(st)
+    out = mk.linear_attention_step(x, cs, cw, st, gg, beta, z, nw, k_heads=hk)
+    mixed = mk.causal_conv1d_update(x, cs2, cw)
+    q = mixed[:, :hk * dk].reshape(batch, hk, dk)
+    k = mixed[:, hk * dk:2 * hk * dk].reshape(batch, hk, dk)
+    v = mixed[:, 2 * hk * dk:].reshape(batch, hv, dv)
+    o, new_state = mk.linear_attention_decode(mk.LinearAttentionInputs(q=q, k=k, v=v, state=st2, g=gg, beta=beta,
+                                                                       qk_l2norm=True))
+    want = mk.gated_rms_norm(o, z, nw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    assert torch.equal(cs, cs2)
+    assert torch.equal(st, new_state)
+    bf = dtype == torch.bfloat16
+    rnd = oracle.bf16_round if bf else (lambda a: a)
+    m, ref_cs = oracle.causal_conv1d_update(np32(x), np_cs, np32(cw), bf16=bf)
+    rq = m[:, :hk * dk].reshape(batch, hk, dk)
+    rk = m[:, hk * dk:2 * hk * dk].reshape(batch, hk, dk)
+    rv = m[:, 2 * hk * dk:].reshape(batch, hv, dv)
+    ro, _ = oracle.gated_delta_decode(rq, rk, rv, np_st, np32(gg), np32(beta), qk_l2norm=True)
+    ref = oracle.gated_rms_norm(rnd(ro), np32(z), np32(nw), bf16=bf)
+    assert_close_out(out, ref)
+    np.testing.assert_array_equal(np32(cs), ref_cs)
+    # The state against the oracle's recurrence on the device's own conv
+    # output (the conv is pinned on its own above; the oracle does not round
+    # to f16 between the ops), to the FP32 state tolerance.
+    _, ref_st = oracle.gated_delta_decode(np32(q), np32(k), np32(v), np_st, np32(gg), np32(beta), qk_l2norm=True)
+    np.testing.assert_allclose(st.cpu().numpy(), ref_st, rtol=1e-4, atol=1e-4)

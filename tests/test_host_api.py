@@ -250,3 +250,26 @@ def test_paged_entry_validates_on_the_host_without_gpu():
                 None) == _lib.MKQ_ERR_INVALID
     assert call(_lib.MKQ_DTYPE_F32, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, ws, nbytes,
                 None) == _lib.MKQ_ERR_UNSUPPORTED
+
+
+def test_linear_step_entry_validates_on_the_host_without_gpu():
+    """mkq_linear_attention_step sizes its workspace from the shapes and
+    rejects a short or misaligned workspace and a key_dim above 256 before
+    any launch."""
+    lib = _lib.load_library()
+    need = lib.mkq_linear_attention_step_workspace_bytes(_lib.MKQ_DTYPE_BF16, 2, 16, 32, 128, 128)
+    c = 2 * 16 * 128 + 32 * 128
+    assert need == ((2 * c * 2 + 255) // 256 + (2 * 32 * 128 * 2 + 255) // 256) * 256
+    assert lib.mkq_linear_attention_step_workspace_bytes(99, 2, 16, 32, 128, 128) == 0
+    raw = ctypes.create_string_buffer(need + 512)
+    ws = (ctypes.addressof(raw) + 255) // 256 * 256
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.addressof(buf)
+    call = lib.mkq_linear_attention_step
+    args = [p, p, p, None, 3, p, p, p, p, p, p, 2, 16, 32, 128, 128, 0.1, 1e-6]
+    assert call(_lib.MKQ_DTYPE_BF16, *args, ws, need - 1, None) == _lib.MKQ_ERR_INVALID
+    assert b"workspace" in lib.mkq_last_error()
+    assert call(_lib.MKQ_DTYPE_BF16, *args, ws + 16, need, None) == _lib.MKQ_ERR_INVALID
+    bad = list(args)
+    bad[14] = 512  # key_dim
+    assert call(_lib.MKQ_DTYPE_BF16, *bad, ws, need, None) == _lib.MKQ_ERR_UNSUPPORTED
