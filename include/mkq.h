@@ -159,6 +159,20 @@ int mkq_full_attention_decode_paged(int dtype, const void* q, const void* k_bloc
                                     int max_blocks, int num_blocks, float scale, void* workspace,
                                     size_t workspace_bytes, void* stream);
 
+/* Paged KV with the KV append fused in: k_new, v_new [batch, kv_heads,
+ * head_dim] are token seq_len - 1 of every batch row and are written (in
+ * place) to row (seq_len - 1) % block_size of block
+ * block_table[b, (seq_len - 1) / block_size]; the result equals writing that
+ * row first and calling mkq_full_attention_decode_paged, bit for bit.  A
+ * block id outside the pool is neither read nor written.  Limits as for the
+ * two entry points it combines.  No counterpart in the reference. */
+int mkq_full_attention_decode_paged_append(int dtype, const void* q, const void* k_new, const void* v_new,
+                                           void* k_blocks, void* v_blocks, const int* block_table,
+                                           void* out, int batch, int q_heads, int kv_heads, int head_dim,
+                                           int seq_len, int block_size, int max_blocks, int num_blocks,
+                                           float scale, void* workspace, size_t workspace_bytes,
+                                           void* stream);
+
 /* ------------------------------------------------------------------------
  * Recurrent linear-attention decode, reference rule.  Replaces
  *   _C.linear_attention_decode    (csrc/bindings.cpp:35, csrc/linear_attention_decode.cu:46-93)

@@ -503,9 +503,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   }
   if constexpr (APP) {
     if (owner && hg == 0 && wave == 0 && lane * 8 < d) {
-      const size_t row = (size_t(b) * cap + (seq - 1)) * hkv * d + size_t(kvh) * d + size_t(lane) * 8;
-      *reinterpret_cast<u32x4*>(kw + row) = kap;
-      *reinterpret_cast<u32x4*>(vw + row) = vap;
+      size_t row = (size_t(b) * cap + (seq - 1)) * hkv * d;
+      bool ok = true;
+      if constexpr (PG) {  // the new row's block id is staged (this chunk holds it)
+        const int blk = blk_l[(seq - 1) / bsz - bi0];
+        ok = blk >= 0 && blk < nblocks;
+        row = (size_t(ok ? blk : 0) * bsz + (seq - 1) % bsz) * hkv * d;
+      }
+      row += size_t(kvh) * d + size_t(lane) * 8;
+      if (ok) {
+        *reinterpret_cast<u32x4*>(kw + row) = kap;
+        *reinterpret_cast<u32x4*>(vw + row) = vap;
+      }
     }
   }
 }
@@ -733,6 +742,8 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
                                     hipFuncAttributeMaxDynamicSharedMemorySize, roped));
     MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, false, true>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, pagedb));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, true, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, pagedb));
     attr_set = true;
   }
   MKQ_REQUIRE(size_t(ch.nch) * units < (size_t(1) << 31), "full_attention_decode: grid too large");
@@ -740,7 +751,7 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   float* part_m = part_o + size_t(batch) * hq * ch.nch * d;
   float* part_l = part_m + size_t(batch) * hq * ch.nch;
   const bool app = ap.k_new != nullptr;
-  auto* kern = paged  ? attn_chunk_kernel<T, DT, false, false, true>
+  auto* kern = paged  ? (app ? attn_chunk_kernel<T, DT, false, true, true> : attn_chunk_kernel<T, DT, false, false, true>)
                : rot > 0 ? (app ? attn_chunk_kernel<T, DT, true, true, false> : attn_chunk_kernel<T, DT, true, false, false>)
                          : (app ? attn_chunk_kernel<T, DT, false, true, false>
                                 : attn_chunk_kernel<T, DT, false, false, false>);
@@ -916,4 +927,28 @@ extern "C" int mkq_full_attention_decode_paged(int dtype, const void* q, const v
   pg.num_blocks = num_blocks;
   return attention_entry(fn, dtype, q, k_blocks, v_blocks, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
                          nullptr, 0, Append{}, pg, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mkq_full_attention_decode_paged_append(int dtype, const void* q, const void* k_new, const void* v_new,
+                                                      void* k_blocks, void* v_blocks, const int* block_table,
+                                                      void* out, int batch, int q_heads, int kv_heads, int head_dim,
+                                                      int seq_len, int block_size, int max_blocks, int num_blocks,
+                                                      float scale, void* workspace, size_t workspace_bytes,
+                                                      void* stream) {
+  const char* fn = "full_attention_decode_paged_append";
+  if (!block_table || !k_new || !v_new) {
+    clear_error();
+    return set_error(MKQ_ERR_INVALID, "%s: null tensor pointer", fn);
+  }
+  Paged pg;
+  pg.table = block_table;
+  pg.block_size = block_size;
+  pg.max_blocks = max_blocks;
+  pg.num_blocks = num_blocks;
+  Append ap;
+  ap.k_new = k_new;
+  ap.v_new = v_new;
+  ap.cap = seq_len;  // unused by the paged store
+  return attention_entry(fn, dtype, q, k_blocks, v_blocks, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
+                         nullptr, 0, ap, pg, workspace, workspace_bytes, stream);
 }

@@ -301,7 +301,8 @@ torch::Tensor full_attention_decode_append(torch::Tensor q, torch::Tensor k_new,
 // q [B, Hq, D]; k_blocks/v_blocks [num_blocks, block_size, Hkv, D];
 // block_table [B, max_blocks] int32; attends over the first seq_len tokens.
 torch::Tensor full_attention_decode_paged(torch::Tensor q, torch::Tensor k_blocks, torch::Tensor v_blocks,
-                                          torch::Tensor block_table, int64_t seq_len, double scale) {
+                                          torch::Tensor block_table, int64_t seq_len, double scale,
+                                          c10::optional<torch::Tensor> k_new, c10::optional<torch::Tensor> v_new) {
   MK_CHECK_INPUT(q);
   MK_CHECK_INPUT(k_blocks);
   MK_CHECK_INPUT(v_blocks);
@@ -326,11 +327,28 @@ torch::Tensor full_attention_decode_paged(torch::Tensor q, torch::Tensor k_block
   auto out = torch::empty_like(q);
   auto ws = workspace_for(Ws::kAttention, q,
                           mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq));
-  const int rc = mkq_full_attention_decode_paged(
-      to_mkq_dtype(q), q.data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(), block_table.data_ptr<int>(),
-      out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq, static_cast<int>(k_blocks.size(1)),
-      static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)), static_cast<float>(scale),
-      ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream());
+  TORCH_CHECK(k_new.has_value() == v_new.has_value(), "k_new and v_new must be given together");
+  int rc;
+  if (k_new.has_value()) {
+    MK_CHECK_INPUT((*k_new));
+    MK_CHECK_INPUT((*v_new));
+    TORCH_CHECK(k_new->dim() == 3 && k_new->size(0) == batch && k_new->size(1) == kv_heads &&
+                    k_new->size(2) == head_dim && v_new->sizes() == k_new->sizes(),
+                "k_new and v_new must be [batch, kv_heads, head_dim]");
+    TORCH_CHECK(k_new->scalar_type() == q.scalar_type() && v_new->scalar_type() == q.scalar_type(),
+                "k_new/v_new dtype mismatch");
+    rc = mkq_full_attention_decode_paged_append(
+        to_mkq_dtype(q), q.data_ptr(), k_new->data_ptr(), v_new->data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(),
+        block_table.data_ptr<int>(), out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq,
+        static_cast<int>(k_blocks.size(1)), static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)),
+        static_cast<float>(scale), ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream());
+  } else {
+    rc = mkq_full_attention_decode_paged(
+        to_mkq_dtype(q), q.data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(), block_table.data_ptr<int>(),
+        out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq, static_cast<int>(k_blocks.size(1)),
+        static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)), static_cast<float>(scale),
+        ws.data_ptr(), static_cast<size_t>(ws.numel()), current_stream());
+  }
   check_status(rc, "full_attention_decode_paged");
   return out;
 }
@@ -599,7 +617,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("scale"), pybind11::arg("cos_sin") = pybind11::none(), pybind11::arg("rotary_dim") = 0);
   m.def("full_attention_decode_paged", &full_attention_decode_paged,
         "Split-K GQA flash-decode over a paged KV pool (HIP)", pybind11::arg("q"), pybind11::arg("k_blocks"),
-        pybind11::arg("v_blocks"), pybind11::arg("block_table"), pybind11::arg("seq_len"), pybind11::arg("scale"));
+        pybind11::arg("v_blocks"), pybind11::arg("block_table"), pybind11::arg("seq_len"), pybind11::arg("scale"),
+        pybind11::arg("k_new") = pybind11::none(), pybind11::arg("v_new") = pybind11::none());
   m.def("linear_attention_decode", &linear_attention_decode, "Recurrent linear-attention decode (HIP)");
   m.def("gated_delta_decode", &gated_delta_decode, "Gated delta rule decode (HIP)", pybind11::arg("q"),
         pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("state"), pybind11::arg("g"), pybind11::arg("beta"),

@@ -372,10 +372,12 @@ def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
     """Attention over a paged KV pool: token t of batch row b is row
     t % block_size of block block_table[b, t // block_size].  The kernel reads
     the blocks in place (bf16/f16, head_dim % 8 == 0, block_size % 16 == 0);
-    other cases gather the rows into a contiguous cache first.  RoPE and the
-    KV append are not combined with the paged layout."""
-    if inputs.k_new is not None or inputs.v_new is not None:
-        raise ValueError("k_new/v_new are not supported with a block_table")
+    other cases gather the rows into a contiguous cache first.  With
+    k_new/v_new the new token is token seq_len - 1 (or cache_seqlen): the
+    kernel writes it into its block and uses it directly; the fallback
+    writes the row first.  RoPE is not combined with the paged layout."""
+    if (inputs.k_new is None) != (inputs.v_new is None):
+        raise ValueError("k_new and v_new must be given together")
     if inputs.cos is not None or inputs.sin is not None:
         raise ValueError("cos/sin are not supported with a block_table")
     kb, vb, table = inputs.k_cache, inputs.v_cache, inputs.block_table
@@ -386,15 +388,32 @@ def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
     if table.dim() != 2 or table.shape[0] != q.shape[0]:
         raise ValueError("block_table must be [batch, max_blocks]")
     seq = int(inputs.seq_len) if inputs.seq_len is not None else table.shape[1] * bs
+    append = inputs.k_new is not None
+    if append and inputs.cache_seqlen is not None:
+        seq = int(inputs.cache_seqlen) + 1
     if not 0 < seq <= table.shape[1] * bs:
         raise ValueError("seq_len must be in [1, max_blocks * block_size]")
     if q.shape[1] % hkv != 0:
         raise ValueError("query_heads must be divisible by kv_heads")
     _require_extension("full_attention_decode", q, kb, vb, table)
     scale = inputs.scale if inputs.scale is not None else 1.0 / math.sqrt(d)
+    if append:
+        if not (kb.is_contiguous() and vb.is_contiguous()):
+            raise ValueError("k_cache and v_cache must be contiguous: the new token is written in place")
+        k_new = inputs.k_new.reshape(q.shape[0], hkv, d)
+        v_new = inputs.v_new.reshape(q.shape[0], hkv, d)
     if kb.dtype in (torch.bfloat16, torch.float16) and d % 8 == 0 and bs % 16 == 0 and q.dtype == kb.dtype:
+        if append:
+            return _C.full_attention_decode_paged(q.contiguous(), kb, vb, table.to(torch.int32).contiguous(), seq,
+                                                  float(scale), k_new.to(kb.dtype).contiguous(),
+                                                  v_new.to(kb.dtype).contiguous())
         return _C.full_attention_decode_paged(q.contiguous(), kb.contiguous(), vb.contiguous(),
                                               table.to(torch.int32).contiguous(), seq, float(scale))
+    if append:  # write the new row into its block first (ids outside the pool are skipped)
+        blk = table[:, (seq - 1) // bs].long()
+        ok = (blk >= 0) & (blk < nblocks)
+        kb[blk[ok], (seq - 1) % bs] = k_new[ok].to(kb.dtype)
+        vb[blk[ok], (seq - 1) % bs] = v_new[ok].to(vb.dtype)
     # Gather the blocks that hold the seq_len tokens; ids outside the pool
     # read as zeros, as in the kernel (never an out-of-range index).
     idx = table[:, : (seq + bs - 1) // bs].long()
@@ -405,7 +424,8 @@ def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
     k = k.reshape(q.shape[0], -1, hkv, d)[:, :seq]
     v = v.reshape(q.shape[0], -1, hkv, d)[:, :seq]
     return full_attention_decode(dataclasses.replace(inputs, k_cache=k, v_cache=v, block_table=None,
-                                                     seq_len=None, scale=scale))
+                                                     seq_len=None, scale=scale, k_new=None, v_new=None,
+                                                     cache_seqlen=None))
 
 
 def full_attention_decode(inputs: FullAttentionInputs) -> torch.Tensor:

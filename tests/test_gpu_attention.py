@@ -403,3 +403,31 @@ def test_attention_paged_fallback_gathers(d, bs, dtype):
     want = mk.full_attention_decode(inp)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t,bs,dtype", [
+    (1, 24, 4, 256, 32768, 16, torch.bfloat16),   # config 4, 16-token blocks
+    (3, 8, 2, 128, 3001, 64, torch.float16),      # ragged last block
+    (2, 40, 2, 128, 1, 16, torch.bfloat16),       # the first token of a fresh block; group 20
+    (2, 4, 2, 128, 77, 8, torch.bfloat16),        # block size the kernel does not take: written first
+])
+def test_attention_paged_append_equals_write_then_attend(b, hq, hkv, d, t, bs, dtype):
+    """KV append into a paged pool: the output and both pools are
+    bit-identical to writing the new row into its block with torch and then
+    attending over the pool; no other row changes."""
+    inp = make_attention(batch=b, q_heads=hq, kv_heads=hkv, head_dim=d, seq_len=t, seed=630 + t, dtype=dtype)
+    pk, pv, table, _, _ = _paged_case(inp, bs, 631 + t)
+    g = torch.Generator().manual_seed(632 + t)
+    k_new = torch.randn(b, hkv, d, generator=g).to("cuda", dtype)
+    v_new = torch.randn(b, hkv, d, generator=g).to("cuda", dtype)
+    pk2, pv2 = pk.clone(), pv.clone()
+    blk = table[:, (t - 1) // bs].long()
+    pk2[blk, (t - 1) % bs] = k_new
+    pv2[blk, (t - 1) % bs] = v_new
+    want = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk2, pv2, scale=inp.scale, block_table=table,
+                                                           seq_len=t))
+    got = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk, pv, scale=inp.scale, block_table=table,
+                                                          seq_len=t, k_new=k_new, v_new=v_new))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(pk, pk2) and torch.equal(pv, pv2)

@@ -273,3 +273,18 @@ def test_linear_step_entry_validates_on_the_host_without_gpu():
     bad = list(args)
     bad[14] = 512  # key_dim
     assert call(_lib.MKQ_DTYPE_BF16, *bad, ws, need, None) == _lib.MKQ_ERR_UNSUPPORTED
+
+
+def test_paged_append_entry_rejects_missing_rows_without_gpu():
+    lib = _lib.load_library()
+    b, hq, hkv, d, t = 1, 4, 2, 64, 40
+    nbytes = lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t)
+    raw = ctypes.create_string_buffer(nbytes + 512)
+    ws = (ctypes.addressof(raw) + 255) // 256 * 256
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    call = lib.mkq_full_attention_decode_paged_append
+    assert call(_lib.MKQ_DTYPE_BF16, p, None, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert call(_lib.MKQ_DTYPE_F32, p, p, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, ws, nbytes,
+                None) == _lib.MKQ_ERR_UNSUPPORTED
