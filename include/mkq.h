@@ -173,6 +173,17 @@ int mkq_full_attention_decode_paged_append(int dtype, const void* q, const void*
                                            float scale, void* workspace, size_t workspace_bytes,
                                            void* stream);
 
+/* Paged KV with q and the keys rotated in the kernel (cos_sin and
+ * rotary_dim as for mkq_full_attention_decode_rope, which must not be NULL);
+ * bit-identical to that entry point over the gathered contiguous cache.
+ * No counterpart in the reference. */
+int mkq_full_attention_decode_paged_rope(int dtype, const void* q, const void* k_blocks,
+                                         const void* v_blocks, const int* block_table, void* out,
+                                         int batch, int q_heads, int kv_heads, int head_dim, int seq_len,
+                                         int block_size, int max_blocks, int num_blocks, float scale,
+                                         const float* cos_sin, int rotary_dim, void* workspace,
+                                         size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Recurrent linear-attention decode, reference rule.  Replaces
  *   _C.linear_attention_decode    (csrc/bindings.cpp:35, csrc/linear_attention_decode.cu:46-93)

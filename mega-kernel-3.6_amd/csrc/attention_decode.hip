@@ -732,6 +732,7 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
     const int plain = int(chunk_lds_bytes<DT>(DT, 16));
     const int roped = int(chunk_lds_bytes<DT>(DT, 16) + 16 + 2 * kMaxD * sizeof(float));
     const int pagedb = int(chunk_lds_bytes<DT>(DT, 16) + 16 + kMaxChunkBlocks * sizeof(int));
+    const int paged_roped = int(pagedb + 2 * kMaxD * sizeof(float));
     MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, false, false>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, plain));
     MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, false, false>),
@@ -744,6 +745,8 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
                                     hipFuncAttributeMaxDynamicSharedMemorySize, pagedb));
     MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, false, true, true>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, pagedb));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, false, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, paged_roped));
     attr_set = true;
   }
   MKQ_REQUIRE(size_t(ch.nch) * units < (size_t(1) << 31), "full_attention_decode: grid too large");
@@ -751,21 +754,23 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   float* part_m = part_o + size_t(batch) * hq * ch.nch * d;
   float* part_l = part_m + size_t(batch) * hq * ch.nch;
   const bool app = ap.k_new != nullptr;
-  auto* kern = paged  ? (app ? attn_chunk_kernel<T, DT, false, true, true> : attn_chunk_kernel<T, DT, false, false, true>)
+  auto* kern = paged  ? (app ? attn_chunk_kernel<T, DT, false, true, true>
+                             : rot > 0 ? attn_chunk_kernel<T, DT, true, false, true>
+                                       : attn_chunk_kernel<T, DT, false, false, true>)
                : rot > 0 ? (app ? attn_chunk_kernel<T, DT, true, true, false> : attn_chunk_kernel<T, DT, true, false, false>)
                          : (app ? attn_chunk_kernel<T, DT, false, true, false>
                                 : attn_chunk_kernel<T, DT, false, false, false>);
-  // The cos/sin table (ROPE) or the block ids (PG) follow the staging/merge area.
+  // The cos/sin table (ROPE) and then the block ids (PG) follow the
+  // staging/merge area.
   const size_t rope_off = (lds + 15) / 16 * 16;
+  const size_t blk_off = rope_off + (rot > 0 ? size_t(2 * rot) * sizeof(float) : 0);
   const int nblk = paged ? (ch.chunk_tokens + pg.block_size - 1) / pg.block_size + 2 : 0;
-  const size_t lds_all = rot > 0 ? rope_off + size_t(2 * rot) * sizeof(float)
-                         : paged ? rope_off + size_t(nblk) * sizeof(int)
-                                 : lds;
+  const size_t lds_all = paged ? blk_off + size_t(nblk) * sizeof(int) : rot > 0 ? blk_off : lds;
   kern<<<dim3(ch.nch * units), kThreads, lds_all, stream>>>(
       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v), part_o, part_m, part_l,
       static_cast<T*>(out), rope_cs, static_cast<const T*>(ap.k_new), static_cast<const T*>(ap.v_new),
       app ? static_cast<T*>(const_cast<void*>(k)) : nullptr, app ? static_cast<T*>(const_cast<void*>(v)) : nullptr,
-      app ? ap.cap : seq, pg.table, pg.block_size, pg.max_blocks, pg.num_blocks, int(rope_off), rot, int(rope_off), hq,
+      app ? ap.cap : seq, pg.table, pg.block_size, pg.max_blocks, pg.num_blocks, int(blk_off), rot, int(rope_off), hq,
       hkv, d, seq, group, ngroups, units, ch.nch, ch.chunk_tokens, scale * kLog2e);
   MKQ_LAUNCH_CHECK("attn_chunk_kernel");
   if (ch.nch > 1) {
@@ -927,6 +932,26 @@ extern "C" int mkq_full_attention_decode_paged(int dtype, const void* q, const v
   pg.num_blocks = num_blocks;
   return attention_entry(fn, dtype, q, k_blocks, v_blocks, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
                          nullptr, 0, Append{}, pg, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mkq_full_attention_decode_paged_rope(int dtype, const void* q, const void* k_blocks,
+                                                    const void* v_blocks, const int* block_table, void* out,
+                                                    int batch, int q_heads, int kv_heads, int head_dim, int seq_len,
+                                                    int block_size, int max_blocks, int num_blocks, float scale,
+                                                    const float* cos_sin, int rotary_dim, void* workspace,
+                                                    size_t workspace_bytes, void* stream) {
+  const char* fn = "full_attention_decode_paged_rope";
+  if (!block_table) {
+    clear_error();
+    return set_error(MKQ_ERR_INVALID, "%s: null tensor pointer", fn);
+  }
+  Paged pg;
+  pg.table = block_table;
+  pg.block_size = block_size;
+  pg.max_blocks = max_blocks;
+  pg.num_blocks = num_blocks;
+  return attention_entry(fn, dtype, q, k_blocks, v_blocks, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
+                         cos_sin, rotary_dim, Append{}, pg, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mkq_full_attention_decode_paged_append(int dtype, const void* q, const void* k_new, const void* v_new,

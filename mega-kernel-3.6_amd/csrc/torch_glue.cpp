@@ -302,7 +302,8 @@ torch::Tensor full_attention_decode_append(torch::Tensor q, torch::Tensor k_new,
 // block_table [B, max_blocks] int32; attends over the first seq_len tokens.
 torch::Tensor full_attention_decode_paged(torch::Tensor q, torch::Tensor k_blocks, torch::Tensor v_blocks,
                                           torch::Tensor block_table, int64_t seq_len, double scale,
-                                          c10::optional<torch::Tensor> k_new, c10::optional<torch::Tensor> v_new) {
+                                          c10::optional<torch::Tensor> k_new, c10::optional<torch::Tensor> v_new,
+                                          c10::optional<torch::Tensor> cos_sin, int64_t rotary_dim) {
   MK_CHECK_INPUT(q);
   MK_CHECK_INPUT(k_blocks);
   MK_CHECK_INPUT(v_blocks);
@@ -328,8 +329,19 @@ torch::Tensor full_attention_decode_paged(torch::Tensor q, torch::Tensor k_block
   auto ws = workspace_for(Ws::kAttention, q,
                           mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq));
   TORCH_CHECK(k_new.has_value() == v_new.has_value(), "k_new and v_new must be given together");
+  TORCH_CHECK(!(k_new.has_value() && cos_sin.has_value()), "the paged append does not take cos_sin");
   int rc;
-  if (k_new.has_value()) {
+  if (cos_sin.has_value()) {
+    TORCH_CHECK(cos_sin->is_cuda() && cos_sin->is_contiguous() && cos_sin->scalar_type() == torch::kFloat32,
+                "cos_sin must be a contiguous float32 device tensor");
+    TORCH_CHECK(cos_sin->numel() == 2 * rotary_dim, "cos_sin must hold 2 * rotary_dim values");
+    rc = mkq_full_attention_decode_paged_rope(
+        to_mkq_dtype(q), q.data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(), block_table.data_ptr<int>(),
+        out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq, static_cast<int>(k_blocks.size(1)),
+        static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)), static_cast<float>(scale),
+        cos_sin->data_ptr<float>(), static_cast<int>(rotary_dim), ws.data_ptr(), static_cast<size_t>(ws.numel()),
+        current_stream());
+  } else if (k_new.has_value()) {
     MK_CHECK_INPUT((*k_new));
     MK_CHECK_INPUT((*v_new));
     TORCH_CHECK(k_new->dim() == 3 && k_new->size(0) == batch && k_new->size(1) == kv_heads &&
@@ -618,7 +630,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("full_attention_decode_paged", &full_attention_decode_paged,
         "Split-K GQA flash-decode over a paged KV pool (HIP)", pybind11::arg("q"), pybind11::arg("k_blocks"),
         pybind11::arg("v_blocks"), pybind11::arg("block_table"), pybind11::arg("seq_len"), pybind11::arg("scale"),
-        pybind11::arg("k_new") = pybind11::none(), pybind11::arg("v_new") = pybind11::none());
+        pybind11::arg("k_new") = pybind11::none(), pybind11::arg("v_new") = pybind11::none(),
+        pybind11::arg("cos_sin") = pybind11::none(), pybind11::arg("rotary_dim") = 0);
   m.def("linear_attention_decode", &linear_attention_decode, "Recurrent linear-attention decode (HIP)");
   m.def("gated_delta_decode", &gated_delta_decode, "Gated delta rule decode (HIP)", pybind11::arg("q"),
         pybind11::arg("k"), pybind11::arg("v"), pybind11::arg("state"), pybind11::arg("g"), pybind11::arg("beta"),

@@ -375,11 +375,11 @@ def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
     other cases gather the rows into a contiguous cache first.  With
     k_new/v_new the new token is token seq_len - 1 (or cache_seqlen): the
     kernel writes it into its block and uses it directly; the fallback
-    writes the row first.  RoPE is not combined with the paged layout."""
+    writes the row first.  With cos/sin, q and the keys are rotated in the
+    kernel where it can (no append); otherwise the rows are gathered and the
+    contiguous path rotates them."""
     if (inputs.k_new is None) != (inputs.v_new is None):
         raise ValueError("k_new and v_new must be given together")
-    if inputs.cos is not None or inputs.sin is not None:
-        raise ValueError("cos/sin are not supported with a block_table")
     kb, vb, table = inputs.k_cache, inputs.v_cache, inputs.block_table
     if kb.dim() != 4 or vb.shape != kb.shape:
         raise ValueError("k_cache and v_cache must be [num_blocks, block_size, kv_heads, head_dim] with a block_table")
@@ -402,7 +402,14 @@ def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
             raise ValueError("k_cache and v_cache must be contiguous: the new token is written in place")
         k_new = inputs.k_new.reshape(q.shape[0], hkv, d)
         v_new = inputs.v_new.reshape(q.shape[0], hkv, d)
-    if kb.dtype in (torch.bfloat16, torch.float16) and d % 8 == 0 and bs % 16 == 0 and q.dtype == kb.dtype:
+    rope = inputs.cos is not None and inputs.sin is not None
+    cs = _rope_in_kernel(inputs) if rope else None
+    if (kb.dtype in (torch.bfloat16, torch.float16) and d % 8 == 0 and bs % 16 == 0 and q.dtype == kb.dtype
+            and not (rope and (append or cs is None))):
+        if rope:
+            return _C.full_attention_decode_paged(q.contiguous(), kb.contiguous(), vb.contiguous(),
+                                                  table.to(torch.int32).contiguous(), seq, float(scale),
+                                                  cos_sin=cs, rotary_dim=int(inputs.rotary_dim))
         if append:
             return _C.full_attention_decode_paged(q.contiguous(), kb, vb, table.to(torch.int32).contiguous(), seq,
                                                   float(scale), k_new.to(kb.dtype).contiguous(),

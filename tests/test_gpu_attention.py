@@ -431,3 +431,24 @@ def test_attention_paged_append_equals_write_then_attend(b, hq, hkv, d, t, bs, d
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.equal(pk, pk2) and torch.equal(pv, pv2)
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t,bs,rot,dtype", [
+    (1, 24, 4, 256, 32768, 16, 64, torch.bfloat16),   # config 4 with RoPE, 16-token blocks
+    (3, 8, 2, 128, 3001, 64, 32, torch.float16),
+    (2, 8, 2, 128, 300, 32, 24, torch.bfloat16),      # rotary_dim the kernel cannot rotate: gathered first
+])
+def test_attention_paged_rope_equals_contiguous_rope(b, hq, hkv, d, t, bs, rot, dtype):
+    """Paged KV with RoPE: bit-identical to the contiguous RoPE path on the
+    same tokens (keys rotated in the kernel where it can, else gathered and
+    rotated as the reference does)."""
+    inp = make_attention(batch=b, q_heads=hq, kv_heads=hkv, head_dim=d, seq_len=t, seed=640 + t, dtype=dtype)
+    pk, pv, table, _, _ = _paged_case(inp, bs, 641 + t)
+    ang = torch.rand(rot, generator=torch.Generator().manual_seed(642)) * 6.0
+    cos, sin = torch.cos(ang)[None], torch.sin(ang)[None]
+    want = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, inp.k_cache, inp.v_cache, cos=cos, sin=sin,
+                                                           rotary_dim=rot, scale=inp.scale))
+    got = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk, pv, cos=cos, sin=sin, rotary_dim=rot,
+                                                          scale=inp.scale, block_table=table, seq_len=t))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
