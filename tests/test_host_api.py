@@ -288,3 +288,27 @@ def test_paged_append_entry_rejects_missing_rows_without_gpu():
                 None) == _lib.MKQ_ERR_INVALID
     assert call(_lib.MKQ_DTYPE_F32, p, p, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, ws, nbytes,
                 None) == _lib.MKQ_ERR_UNSUPPORTED
+
+
+def test_new_python_entry_points_validate_arguments_before_device_work():
+    """The paged-KV, conv-update and q/k-norm options reject bad arguments
+    with ValueError before touching a device (CPU tensors here)."""
+    q = torch.zeros(2, 4, 64)
+    pool = torch.zeros(10, 16, 2, 64)
+    with pytest.raises(ValueError, match="block_table"):
+        mk.full_attention_decode(mk.FullAttentionInputs(q, pool, pool.clone(),
+                                                        block_table=torch.zeros(3, 4, dtype=torch.int32)))
+    with pytest.raises(ValueError, match="seq_len"):
+        mk.full_attention_decode(mk.FullAttentionInputs(q, pool, pool.clone(),
+                                                        block_table=torch.zeros(2, 4, dtype=torch.int32),
+                                                        seq_len=65))
+    with pytest.raises(ValueError, match="together"):
+        mk.full_attention_decode(mk.FullAttentionInputs(q, pool, pool.clone(),
+                                                        block_table=torch.zeros(2, 4, dtype=torch.int32),
+                                                        k_new=torch.zeros(2, 2, 64)))
+    with pytest.raises(ValueError, match="activation"):
+        mk.causal_conv1d_update(torch.zeros(1, 8), torch.zeros(1, 8, 3), torch.zeros(8, 4), activation="gelu")
+    lin = mk.LinearAttentionInputs(q=torch.zeros(1, 2, 8), k=torch.zeros(1, 2, 8), v=torch.zeros(1, 2, 8),
+                                   state=torch.zeros(1, 2, 8, 8), qk_l2norm=True)
+    with pytest.raises(ValueError, match="qk_l2norm"):
+        mk.linear_attention_decode(lin)
