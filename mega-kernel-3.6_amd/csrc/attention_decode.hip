@@ -851,6 +851,9 @@ int attention_entry(const char* fn, int dtype, const void* q, const void* k_cach
       return set_error(MKQ_ERR_UNSUPPORTED,
                        "%s: the in-kernel append needs bf16/f16, head_dim %% 8 == 0 and 16-byte aligned tensors", fn);
   }
+  if (pg.table && ap.k_new && rot > 0)
+    return set_error(MKQ_ERR_UNSUPPORTED, "%s: paged KV with both the append and RoPE in one launch is not supported",
+                     fn);
   if (rot > 0) {
     MKQ_REQUIRE(rope_cs, "%s: null cos/sin pointer", fn);
     if (!fast_ok || (dtype != MKQ_DTYPE_BF16 && dtype != MKQ_DTYPE_F16) || rot < 16 || rot > head_dim ||
@@ -941,9 +944,13 @@ extern "C" int mkq_full_attention_decode_paged_rope(int dtype, const void* q, co
                                                     const float* cos_sin, int rotary_dim, void* workspace,
                                                     size_t workspace_bytes, void* stream) {
   const char* fn = "full_attention_decode_paged_rope";
-  if (!block_table) {
+  if (!block_table || !cos_sin) {
     clear_error();
     return set_error(MKQ_ERR_INVALID, "%s: null tensor pointer", fn);
+  }
+  if (rotary_dim <= 0) {
+    clear_error();
+    return set_error(MKQ_ERR_INVALID, "%s: rotary_dim %d must be positive", fn, rotary_dim);
   }
   Paged pg;
   pg.table = block_table;

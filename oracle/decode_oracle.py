@@ -55,6 +55,7 @@ __all__ = [
     "gated_delta_decode",
     "causal_conv1d_update",
     "gated_rms_norm",
+    "attention_cache_view",
     "decode_layer",
     "PINNING",
 ]
@@ -371,6 +372,67 @@ def gated_rms_norm(x, gate, weight, *, eps=1e-6, bf16=True):
     return rnd(t * silu(as_f32(gate)))
 
 
+def attention_cache_view(fa: dict):
+    """The contiguous [B, T, Hkv, D] float32 caches that one attention step
+    reads, given the fields of ``FullAttentionInputs`` as a dict.
+
+    The reference reads ``k_cache``/``v_cache`` as they are (ops.py:367-374).
+    The two optional layouts of this build are restated as their definitions:
+
+    * ``k_new``/``v_new`` (KV append): the new token's key and value
+      [B, Hkv, D] are written to row ``cache_seqlen`` (default: the last row)
+      of copies of the caches, and the first ``cache_seqlen + 1`` tokens are
+      read;
+    * ``block_table`` [B, max_blocks] (paged KV): the caches are block pools
+      [num_blocks, block_size, Hkv, D]; token t of row b is row
+      ``t % block_size`` of block ``block_table[b, t // block_size]``; a block
+      id outside the pool reads as zeros and is never written.  ``seq_len``
+      tokens are read (default max_blocks * block_size; with an append,
+      ``cache_seqlen + 1`` when given).
+    """
+    kc, vc = as_f32(fa["k_cache"]), as_f32(fa["v_cache"])
+    k_new, v_new = fa.get("k_new"), fa.get("v_new")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new must be given together")
+    table = fa.get("block_table")
+    if table is None:
+        if k_new is None:
+            return kc, vc
+        b, cap, hkv, d = kc.shape
+        pos = cap - 1 if fa.get("cache_seqlen") is None else int(fa["cache_seqlen"])
+        if not 0 <= pos < cap:
+            raise ValueError("cache_seqlen must leave room for the new token")
+        kc, vc = kc.copy(), vc.copy()
+        kc[:, pos] = as_f32(k_new).reshape(b, hkv, d)
+        vc[:, pos] = as_f32(v_new).reshape(b, hkv, d)
+        return kc[:, :pos + 1], vc[:, :pos + 1]
+    table = np.asarray(table).astype(np.int64)
+    nblocks, bs, hkv, d = kc.shape
+    batch, max_blocks = table.shape
+    seq = max_blocks * bs if fa.get("seq_len") is None else int(fa["seq_len"])
+    if k_new is not None and fa.get("cache_seqlen") is not None:
+        seq = int(fa["cache_seqlen"]) + 1
+    if not 0 < seq <= max_blocks * bs:
+        raise ValueError("seq_len must be in [1, max_blocks * block_size]")
+    if k_new is not None:
+        kc, vc = kc.copy(), vc.copy()
+        kn, vn = as_f32(k_new).reshape(batch, hkv, d), as_f32(v_new).reshape(batch, hkv, d)
+        for b in range(batch):
+            blk = table[b, (seq - 1) // bs]
+            if 0 <= blk < nblocks:
+                kc[blk, (seq - 1) % bs] = kn[b]
+                vc[blk, (seq - 1) % bs] = vn[b]
+    k = np.zeros((batch, seq, hkv, d), np.float32)
+    v = np.zeros((batch, seq, hkv, d), np.float32)
+    for b in range(batch):
+        for t in range(seq):
+            blk = table[b, t // bs]
+            if 0 <= blk < nblocks:
+                k[b, t] = kc[blk, t % bs]
+                v[b, t] = vc[blk, t % bs]
+    return k, v
+
+
 # ---------------------------------------------------------------------------
 # decode_layer composition  (ops.py:701-748)
 # ---------------------------------------------------------------------------
@@ -404,8 +466,9 @@ def decode_layer(
         if full_attention is None:
             raise ValueError("full_attention inputs are required for full_attention layers")
         fa = full_attention
-        q, kc = apply_partial_rope(fa["q"], fa["k_cache"], fa.get("cos"), fa.get("sin"), fa.get("rotary_dim", 64))
-        a = rnd(full_attention_decode(q, kc, fa["v_cache"], scale=fa.get("scale")))
+        k_cache, v_cache = attention_cache_view(fa)
+        q, kc = apply_partial_rope(fa["q"], k_cache, fa.get("cos"), fa.get("sin"), fa.get("rotary_dim", 64))
+        a = rnd(full_attention_decode(q, kc, v_cache, scale=fa.get("scale")))
         if fa.get("out_proj") is not None:
             a = rnd(a.reshape(a.shape[0], -1) @ as_f32(fa["out_proj"]).T)
         a = a.reshape(h.shape)
@@ -416,8 +479,11 @@ def decode_layer(
             raise ValueError("linear_attention inputs are required for linear_attention layers")
         la = linear_attention
         if la.get("g") is not None:
-            o, s = gated_delta_decode(la["q"], la["k"], la["v"], la["state"], la["g"], la["beta"])
+            o, s = gated_delta_decode(la["q"], la["k"], la["v"], la["state"], la["g"], la["beta"],
+                                      qk_l2norm=bool(la.get("qk_l2norm", False)), q_scale=la.get("q_scale"))
         else:
+            if la.get("qk_l2norm"):
+                raise ValueError("qk_l2norm needs the gated delta rule (g and beta)")
             o, s = linear_attention_decode(la["q"], la["k"], la["v"], la["state"], decay=la.get("decay", 1.0))
         o = rnd(o)
         if la.get("out_proj") is not None:
@@ -465,5 +531,11 @@ PINNING = {
                             "and no activation => out = x and the state shifts by one",
     "gated_rms_norm": "transformers' Qwen3NextRMSNormGated on float32 and bfloat16; constant rows => "
                       "weight * sign(x) * silu(gate)",
-    "decode_layer": "composition of pinned ops; dispatch errors match ops.py:720-739",
+    "attention_cache_view": "append: the written row reads back and every other row is untouched; paged: "
+                            "a shuffled pool of blocks gathers back to the contiguous cache it was cut from, "
+                            "out-of-pool ids read as zeros",
+    "decode_layer": "float64 torch composition of ops.py:701-748 (library attention, transformers' gated "
+                    "delta loop, float64 SwiGLU/MoE) with and without bf16 rounding between ops; zero out_proj "
+                    "=> MoE of the input; zero-gate dense FFN => round(hidden + mixer output); the reshape "
+                    "path; ValueError texts of ops.py:720-739",
 }

@@ -57,6 +57,58 @@ def test_decode_layer_gated_delta_with_moe(batch):
     assert torch.equal(lin.state, state_before)  # the layer returns a new state
 
 
+@pytest.mark.parametrize("batch", [1, 8])
+def test_decode_layer_gated_delta_qk_l2norm_with_moe(batch):
+    """Config 5 with the model's in-kernel q/k L2 norm (unnormalised q and k,
+    q scaled by 1/sqrt(Dk)) composed with the config-2 MoE."""
+    x, w, k = make_moe(batch=batch, seed=160 + batch)
+    lin = make_gated_delta(batch=batch, seed=170 + batch)
+    g = torch.Generator().manual_seed(180 + batch)
+    q = (torch.randn(batch, 16, 128, generator=g) * 2.0).to("cuda", torch.bfloat16)
+    kk = (torch.randn(batch, 16, 128, generator=g) * 0.5).to("cuda", torch.bfloat16)
+    lin = dataclasses.replace(lin, q=q, k=kk, qk_l2norm=True, out_proj=_proj(x.shape[1], 32 * 128, 190 + batch))
+    res = mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+    ref = oracle.decode_layer(
+        np32(x), kind="linear_attention", moe=_np_fields(w, MOE_FIELDS), top_k=k,
+        linear_attention=dict(q=np32(q), k=np32(kk), v=np32(lin.v), state=np32(lin.state), g=np32(lin.g),
+                              beta=np32(lin.beta), out_proj=np32(lin.out_proj), qk_l2norm=True))
+    assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
+    assert_close_state(res.linear_state, ref["linear_state"])
+    assert_close_out(res.linear_output, ref["linear_output"])
+    assert_close_out(res.hidden, ref["hidden"])
+
+
+@pytest.mark.parametrize("layout", ["append", "paged_append"])
+def test_decode_layer_attention_append_with_moe(layout):
+    """A full-attention layer whose new token is appended inside the attention
+    kernel, contiguous or paged (16-token blocks in a shuffled pool), against
+    the oracle's decode_layer over the same cache layout."""
+    x, w, k = make_moe(batch=2, seed=200)
+    att = make_attention(batch=2, seq_len=1000, seed=201)
+    g = torch.Generator().manual_seed(202)
+    k_new = torch.randn(2, 4, 256, generator=g).to("cuda", torch.bfloat16)
+    v_new = torch.randn(2, 4, 256, generator=g).to("cuda", torch.bfloat16)
+    proj = _proj(x.shape[1], 24 * 256, 203)
+    if layout == "append":
+        kc, vc = att.k_cache.clone(), att.v_cache.clone()
+        fields = dict(k_cache=kc, v_cache=vc, k_new=k_new, v_new=v_new, cache_seqlen=700)
+    else:
+        bs, nb = 16, (1000 + 15) // 16
+        perm = torch.randperm(4 * nb, generator=g)[: 2 * nb].reshape(2, nb).to(torch.int32)
+        kp = torch.randn(4 * nb, bs, 4, 256, generator=g).to("cuda", torch.bfloat16)
+        vp = torch.randn(4 * nb, bs, 4, 256, generator=g).to("cuda", torch.bfloat16)
+        fields = dict(k_cache=kp, v_cache=vp, k_new=k_new, v_new=v_new, block_table=perm.to("cuda"), seq_len=977)
+    ref_fields = {n: (np32(t) if isinstance(t, torch.Tensor) else t) for n, t in fields.items()}
+    att = dataclasses.replace(att, out_proj=proj, **fields)
+    ref = oracle.decode_layer(
+        np32(x), kind="full_attention", moe=_np_fields(w, MOE_FIELDS), top_k=k,
+        full_attention=dict(q=np32(att.q), scale=att.scale, out_proj=np32(proj), **ref_fields))
+    res = mk.decode_layer(3, x, w, full_attention=att, top_k=k)
+    assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
+    assert_close_out(res.attention_output, ref["attention_output"])
+    assert_close_out(res.hidden, ref["hidden"])
+
+
 def test_decode_layer_full_attention_with_moe():
     """Layer 3 is a full-attention layer: config-4 GQA (T = 4096) then the MoE."""
     x, w, k = make_moe(batch=1, seed=91)

@@ -5,6 +5,8 @@ against the oracle run on FP32 upcasts of the inputs; router weights (FP32)
 atol 1e-5 / rtol 1e-4.
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -159,3 +161,101 @@ def test_moe_many_launches_bit_identical(batch):
     ref, ref_idx, _ = _oracle(x, w, k)
     assert first[1].cpu().tolist() == ref_idx.tolist()
     assert_close_out(first[0], ref)
+
+
+# ---------------------------------------------------------------------------
+# top-k ties: descending logit, the lower expert index first (the strict `>`
+# of the reference kernel's scan, persistent_moe_decode.cu:333; torch.topk
+# order, reference.py:44)
+# ---------------------------------------------------------------------------
+
+def _exact_logits(x, w):
+    """Router logits in float64, one dot per (row, expert), so identical router
+    rows give identical values."""
+    args, _ = moe_oracle_args(x, w)
+    xn = oracle.rms_norm(args[0], args[1]).astype(np.float64)
+    r = args[2].astype(np.float64)
+    return np.array([[float(np.dot(xn[b], r[e])) for e in range(r.shape[0])] for b in range(xn.shape[0])])
+
+
+def _with_router(w, router):
+    return dataclasses.replace(w, router_weight=router.contiguous())
+
+
+@pytest.mark.parametrize("shape", ["config1", "config2"])
+@pytest.mark.parametrize("batch", [1, 3])
+def test_moe_all_router_rows_tied(shape, batch):
+    """Identical router rows: every logit ties, so the selection is experts
+    0 .. k-1 in that order with equal weights 1/k."""
+    if shape == "config1":
+        x, w, k = make_moe(batch=batch, hidden=512, experts=8, intermediate=256, shared_intermediate=256, top_k=2,
+                           seed=21)
+    else:
+        x, w, k = make_moe(batch=batch, seed=22)
+    w = _with_router(w, w.router_weight[:1].repeat(w.router_weight.shape[0], 1))
+    out, idx, rw = mk.moe_decode(x, w, top_k=k)
+    assert idx.cpu().tolist() == [list(range(k))] * batch
+    torch.testing.assert_close(rw.cpu(), torch.full((batch, k), 1.0 / k), atol=1e-6, rtol=0)
+    ref, ref_idx, _ = _oracle(x, w, k)
+    assert ref_idx.tolist() == idx.cpu().tolist()
+    assert_close_out(out, ref)
+
+
+def _tied_case(batch, seed):
+    """Config 2 with three tie groups planted in row 0's ranking: the top
+    expert duplicated at a higher index, the third at a lower index (both
+    pairs inside the selection) and the expert that lands on rank k
+    duplicated at a lower and a higher index (a tie across the selection
+    boundary).  Returns None when the seed's logits have accidental near-ties
+    (within 1e-4) among the top k + 4, which FP32 could order differently."""
+    x, w, k = make_moe(batch=batch, seed=seed)
+    lg = _exact_logits(x, w)
+    r = np.argsort(-lg[0], kind="stable")
+    far = [int(e) for e in r[k + 4:]]
+    e1, e3, eb = int(r[0]), int(r[2]), int(r[k - 3])
+    try:
+        j_hi = next(e for e in far if e > e1)
+        j_lo = next(e for e in far if e < e3 and e != j_hi)
+        j_blo = next(e for e in far if e < eb and e not in (j_hi, j_lo))
+        j_bhi = next(e for e in far if e > eb and e not in (j_hi, j_lo, j_blo))
+    except StopIteration:
+        return None
+    router = w.router_weight.clone()
+    for dst, src in ((j_hi, e1), (j_lo, e3), (j_blo, eb), (j_bhi, eb)):
+        router[dst] = router[src]
+    w = _with_router(w, router)
+    lg = _exact_logits(x, w)
+    for b in range(batch):
+        top = np.unique(np.sort(lg[b])[::-1][: k + 4])
+        if np.min(np.diff(top)) <= 1e-4:
+            return None
+    expect = np.argsort(-lg, axis=-1, kind="stable")[:, :k]
+    row0 = expect[0].tolist()
+    # the planted structure is where it was meant to be
+    assert row0.index(j_hi) == row0.index(e1) + 1 and row0.index(e3) == row0.index(j_lo) + 1
+    assert row0[k - 1] == j_blo and eb not in row0 and j_bhi not in row0
+    assert lg[0, eb] == lg[0, j_blo]
+    return x, w, k, expect
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_moe_topk_ties_lower_index_first(batch):
+    case = None
+    for seed in range(500, 540):
+        case = _tied_case(batch, seed)
+        if case is not None:
+            break
+    assert case is not None, "no seed without accidental near-ties"
+    x, w, k, expect = case
+    out, idx, rw = mk.moe_decode(x, w, top_k=k)
+    assert idx.cpu().tolist() == expect.tolist()
+    rw = rw.cpu()
+    row0 = expect[0].tolist()
+    lg = _exact_logits(x, w)[0]
+    for a, b in zip(row0, row0[1:]):
+        if lg[a] == lg[b]:  # tied slots carry bit-identical weights
+            assert rw[0, row0.index(a)] == rw[0, row0.index(b)]
+    ref, ref_idx, ref_w = _oracle(x, w, k)
+    assert ref_idx.tolist() == expect.tolist()
+    torch.testing.assert_close(rw, torch.from_numpy(np.asarray(ref_w, np.float32)), atol=1e-5, rtol=1e-4)
+    assert_close_out(out, ref)

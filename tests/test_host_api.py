@@ -290,6 +290,35 @@ def test_paged_append_entry_rejects_missing_rows_without_gpu():
                 None) == _lib.MKQ_ERR_UNSUPPORTED
 
 
+def test_paged_rope_entry_validates_on_the_host_without_gpu():
+    """mkq_full_attention_decode_paged_rope checks its arguments before any
+    launch: a null table or cos/sin and a non-positive rotary_dim or a block
+    size that is not a multiple of 16 (INVALID); FP32 and a rotary_dim that is
+    not a power of two in [16, head_dim] (UNSUPPORTED).  Host buffers, never
+    touched."""
+    lib = _lib.load_library()
+    b, hq, hkv, d, t = 1, 4, 2, 64, 40
+    nbytes = lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t)
+    raw = ctypes.create_string_buffer(nbytes + 512)
+    ws = (ctypes.addressof(raw) + 255) // 256 * 256
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    call = lib.mkq_full_attention_decode_paged_rope
+
+    def run(dtype=_lib.MKQ_DTYPE_BF16, table=p, cs=p, block_size=16, rot=32):
+        return call(dtype, p, p, p, table, p, b, hq, hkv, d, t, block_size, 3, 8, 1.0, cs, rot, ws, nbytes, None)
+
+    assert run(table=None) == _lib.MKQ_ERR_INVALID
+    assert run(cs=None) == _lib.MKQ_ERR_INVALID
+    assert run(rot=0) == _lib.MKQ_ERR_INVALID
+    assert b"rotary_dim" in lib.mkq_last_error()
+    assert run(block_size=24) == _lib.MKQ_ERR_INVALID
+    assert run(dtype=_lib.MKQ_DTYPE_F32) == _lib.MKQ_ERR_UNSUPPORTED
+    for rot in (8, 48, 128):  # below 16, not a power of two, above head_dim
+        assert run(rot=rot) == _lib.MKQ_ERR_UNSUPPORTED
+        assert b"rotary_dim" in lib.mkq_last_error()
+
+
 def test_new_python_entry_points_validate_arguments_before_device_work():
     """The paged-KV, conv-update and q/k-norm options reject bad arguments
     with ValueError before touching a device (CPU tensors here)."""

@@ -304,6 +304,34 @@ def test_gated_delta_qk_l2norm_matches_transformers():
     np.testing.assert_allclose(s2, state.float().numpy(), rtol=1e-5, atol=1e-5)
 
 
+def test_gated_delta_qk_l2norm_bf16_inputs_vs_transformers_bf16_loop():
+    """The in-kernel q/k L2 norm is taken in FP32 on the upcast inputs, as the
+    fused recurrent kernel of flash-linear-attention does with
+    use_qk_l2norm_in_kernel.  transformers' torch fallback normalises in the
+    input dtype (x*x, the sum, rsqrt and the product each rounded to bf16)
+    before its float32 cast.  On bf16 config-5 inputs the two agree on the
+    output within the bf16 tolerance (measured max 1.6e-4 abs) and on the
+    FP32 state within 5e-3 abs (measured 3.0e-3): the difference is the bf16
+    rounding of the normalised q and k, which the FP32 target does not do."""
+    tr = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    r = np.random.default_rng(0)
+    b, hk, hv, dk, dv = 2, 16, 32, 128, 128
+    q, k, v = (oracle.bf16_round(r.standard_normal(sh).astype(np.float32))
+               for sh in ((b, hk, dk), (b, hk, dk), (b, hv, dv)))
+    s = (r.standard_normal((b, hv, dk, dv)) * 0.1).astype(np.float32)
+    g = -np.log1p(np.exp(r.standard_normal((b, hv)))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-r.standard_normal((b, hv))))).astype(np.float32)
+    o, s2 = oracle.gated_delta_decode(q, k, v, s, g, beta, qk_l2norm=True)
+    rep, bf = hv // hk, torch.bfloat16
+    out, state = tr.torch_recurrent_gated_delta_rule(
+        torch.from_numpy(np.repeat(q, rep, 1))[:, None].to(bf), torch.from_numpy(np.repeat(k, rep, 1))[:, None].to(bf),
+        torch.from_numpy(v)[:, None].to(bf), torch.from_numpy(g)[:, None], torch.from_numpy(beta)[:, None],
+        torch.from_numpy(s), True, use_qk_l2norm_in_kernel=True)
+    np.testing.assert_allclose(o, out[:, 0].float().numpy(), rtol=1e-2, atol=1e-2)
+    np.testing.assert_allclose(s2, state.float().numpy(), rtol=0, atol=5e-3)
+    assert not np.allclose(s2, state.float().numpy(), rtol=0, atol=1e-4)  # the rounding is visible
+
+
 def test_causal_conv1d_update_identity_tap_and_shift():
     """With only the newest tap set to 1 and no activation the output is the
     input, and the state shifts by one token with the input appended."""
@@ -408,7 +436,253 @@ def test_golden_gated_delta():
     np.testing.assert_allclose(s, g["new_state"], rtol=1e-5, atol=1e-6)
 
 
+# ---------------------------------------------------------------------------
+# attention cache layouts (KV append, paged KV)
+# ---------------------------------------------------------------------------
+
+def test_attention_cache_view_append_writes_one_row():
+    b, cap, hkv, d = 2, 7, 2, 8
+    kc, vc = randn(b, cap, hkv, d), randn(b, cap, hkv, d)
+    kn, vn = randn(b, hkv, d), randn(b, hkv, d)
+    for pos in (None, 3, 0):
+        k, v = oracle.attention_cache_view(dict(k_cache=kc, v_cache=vc, k_new=kn, v_new=vn, cache_seqlen=pos))
+        p = cap - 1 if pos is None else pos
+        assert k.shape == (b, p + 1, hkv, d)
+        np.testing.assert_array_equal(k[:, p], kn)
+        np.testing.assert_array_equal(v[:, p], vn)
+        np.testing.assert_array_equal(k[:, :p], kc[:, :p])
+        np.testing.assert_array_equal(v[:, :p], vc[:, :p])
+    np.testing.assert_array_equal(oracle.attention_cache_view(dict(k_cache=kc, v_cache=vc))[0], kc)
+    with pytest.raises(ValueError, match="cache_seqlen must leave room"):
+        oracle.attention_cache_view(dict(k_cache=kc, v_cache=vc, k_new=kn, v_new=vn, cache_seqlen=cap))
+    with pytest.raises(ValueError, match="given together"):
+        oracle.attention_cache_view(dict(k_cache=kc, v_cache=vc, k_new=kn))
+
+
+def test_attention_cache_view_paged_gathers_the_cut_cache():
+    """Cut a contiguous cache into blocks, scatter them over a shuffled pool
+    with garbage in the unused blocks: the paged view gathers the original
+    back; an out-of-pool id reads as zeros; an append lands in its block."""
+    b, t, hkv, d, bs = 2, 40, 2, 8, 16
+    nb_row = (t + bs - 1) // bs
+    kc, vc = randn(b, nb_row * bs, hkv, d), randn(b, nb_row * bs, hkv, d)
+    pool_n = 2 * b * nb_row
+    perm = np.random.default_rng(5).permutation(pool_n)[: b * nb_row].reshape(b, nb_row)
+    kp, vp = randn(pool_n, bs, hkv, d), randn(pool_n, bs, hkv, d)
+    for r in range(b):
+        for j in range(nb_row):
+            kp[perm[r, j]] = kc[r, j * bs:(j + 1) * bs]
+            vp[perm[r, j]] = vc[r, j * bs:(j + 1) * bs]
+    k, v = oracle.attention_cache_view(dict(k_cache=kp, v_cache=vp, block_table=perm.astype(np.int32), seq_len=t))
+    np.testing.assert_array_equal(k, kc[:, :t])
+    np.testing.assert_array_equal(v, vc[:, :t])
+    bad = perm.copy()
+    bad[1, 1] = pool_n + 3
+    k, _ = oracle.attention_cache_view(dict(k_cache=kp, v_cache=vp, block_table=bad, seq_len=t))
+    assert np.all(k[1, bs:2 * bs] == 0) and np.array_equal(k[0], kc[0, :t])
+    kn, vn = randn(b, hkv, d), randn(b, hkv, d)
+    k, v = oracle.attention_cache_view(dict(k_cache=kp, v_cache=vp, block_table=perm, seq_len=t, k_new=kn, v_new=vn))
+    np.testing.assert_array_equal(k[:, t - 1], kn)
+    np.testing.assert_array_equal(k[:, : t - 1], kc[:, : t - 1])
+
+
+# ---------------------------------------------------------------------------
+# decode_layer: an independent float64 torch composition of ops.py:701-748
+# ---------------------------------------------------------------------------
+
+def _bf(t, on):
+    return t.to(torch.bfloat16).to(torch.float64) if on else t
+
+
+def _moe64(x, m, k):
+    """MoE in float64 torch (library ops), shared gate on the post-norm input."""
+    xn = F.rms_norm(x, (x.shape[1],), weight=t64(m["norm_weight"]), eps=1e-6)
+    tv, ti = torch.topk(F.linear(xn, t64(m["router_weight"])), k, dim=-1)
+    tw = torch.softmax(tv, -1)
+    shared = _swiglu64(xn, t64(m["shared_gate"]), t64(m["shared_up"]), t64(m["shared_down"]))
+    if m.get("shared_expert_gate") is not None:
+        shared = shared * torch.sigmoid(xn @ t64(m["shared_expert_gate"]).reshape(-1, 1))
+    out = x + shared
+    for b in range(x.shape[0]):
+        for s in range(k):
+            e = int(ti[b, s])
+            out[b] += tw[b, s] * _swiglu64(xn[b:b + 1], t64(m["expert_gate"][e]), t64(m["expert_up"][e]),
+                                           t64(m["expert_down"][e]))[0]
+    return out, ti
+
+
+def _gdr64(la):
+    """Gated delta rule through transformers' recurrent loop (it scales q by
+    1/sqrt(dk), undone here when q/k are not normalised in the kernel)."""
+    tr = pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    q, k, v = t64(la["q"]), t64(la["k"]), t64(la["v"])
+    rep = v.shape[1] // q.shape[1]
+    dk = q.shape[-1]
+    l2 = bool(la.get("qk_l2norm", False))
+    if l2:
+        scale = la.get("q_scale") or 1.0 / math.sqrt(dk)
+        q = q * (scale * math.sqrt(dk))  # q's own length is normalised away; only the scale remains
+    else:
+        q = q * math.sqrt(dk)
+    out, state = tr.torch_recurrent_gated_delta_rule(
+        q.repeat_interleave(rep, 1)[:, None], k.repeat_interleave(rep, 1)[:, None], v[:, None],
+        t64(la["g"])[:, None], t64(la["beta"])[:, None], t64(la["state"]), True, use_qk_l2norm_in_kernel=l2)
+    return out[:, 0], state
+
+
+def _decode_layer64(hidden, kind, *, moe=None, dense=None, attn=None, lin=None, k=8, rounding=False):
+    h = t64(hidden)
+    if kind == "full_attention":
+        q, kc, vc = t64(attn["q"]), t64(attn["k_cache"]), t64(attn["v_cache"])
+        a = F.scaled_dot_product_attention(q[:, :, None], kc.transpose(1, 2), vc.transpose(1, 2),
+                                           scale=attn.get("scale"), enable_gqa=True)[:, :, 0]
+        mixer = _bf(a, rounding)
+    else:
+        mixer, state = _gdr64(lin)
+        mixer = _bf(mixer, rounding)
+    proj = (attn if kind == "full_attention" else lin).get("out_proj")
+    mixer = mixer.reshape(h.shape[0], -1)
+    if proj is not None:
+        mixer = _bf(F.linear(mixer, t64(proj)), rounding)
+    mixer = mixer.reshape(h.shape)
+    resid = _bf(h + mixer, rounding)
+    if dense is not None:
+        xn = F.rms_norm(resid, (h.shape[1],), weight=t64(dense["norm_weight"]), eps=1e-6)
+        return resid + _swiglu64(xn, t64(dense["gate_weight"]), t64(dense["up_weight"]), t64(dense["down_weight"])), \
+            None, mixer
+    out, idx = _moe64(resid, moe, k)
+    return out, idx, mixer
+
+
+def _layer_inputs(B=2, H=32, heads=4, dk=8, dv=16, seed=0):
+    r = np.random.default_rng(seed)
+
+    def rn(*shape, scale=1.0):
+        return (r.standard_normal(shape) * scale).astype(np.float32)
+
+    moe = dict(norm_weight=rn(H, scale=0.1) + 1, router_weight=rn(12, H, scale=0.3),
+               expert_gate=rn(12, 10, H, scale=0.3), expert_up=rn(12, 10, H, scale=0.3),
+               expert_down=rn(12, H, 10, scale=0.3), shared_gate=rn(14, H, scale=0.3),
+               shared_up=rn(14, H, scale=0.3), shared_down=rn(H, 14, scale=0.3),
+               shared_expert_gate=rn(H, scale=0.3))
+    dense = dict(norm_weight=rn(H, scale=0.1) + 1, gate_weight=rn(40, H, scale=0.3), up_weight=rn(40, H, scale=0.3),
+                 down_weight=rn(H, 40, scale=0.3))
+    lin = dict(q=_unit(rn(B, heads // 2, dk)), k=_unit(rn(B, heads // 2, dk)), v=rn(B, heads, dv),
+               state=rn(B, heads, dk, dv, scale=0.1), g=-np.abs(rn(B, heads)),
+               beta=(1 / (1 + np.exp(-rn(B, heads)))).astype(np.float32), out_proj=rn(H, heads * dv, scale=0.2))
+    attn = dict(q=rn(B, 8, dk), k_cache=rn(B, 9, 2, dk), v_cache=rn(B, 9, 2, dk), scale=0.4,
+                out_proj=rn(H, 8 * dk, scale=0.2))
+    return rn(B, H), moe, dense, lin, attn
+
+
+@pytest.mark.parametrize("rounding", [False, True])
+@pytest.mark.parametrize("ffn", ["moe", "dense"])
+@pytest.mark.parametrize("kind", ["linear_attention", "full_attention"])
+def test_decode_layer_matches_float64_composition(kind, ffn, rounding):
+    """oracle.decode_layer against ops.py:701-748 composed from library ops in
+    float64: mixer, then out_proj, then the residual add, then the FFN/MoE
+    with its own residual.  With rounding, both round to bfloat16 at the same
+    points (mixer output, projection, residual sum)."""
+    pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    x, moe, dense, lin, attn = _layer_inputs(seed=3)
+    if rounding:
+        x = oracle.bf16_round(x)
+    mix = dict(linear_attention=lin) if kind == "linear_attention" else dict(full_attention=attn)
+    ffn_kw = dict(moe=moe) if ffn == "moe" else dict(dense_ffn=dense)
+    res = oracle.decode_layer(x, kind=kind, top_k=3, round_to_bf16=rounding, **mix, **ffn_kw)
+    ref, idx, mixer = _decode_layer64(x, kind, moe=moe if ffn == "moe" else None, dense=dense if ffn == "dense" else None,
+                                      attn=attn, lin=lin, k=3, rounding=rounding)
+    tol = 2e-2 if rounding else 2e-4
+    np.testing.assert_allclose(res["hidden"], ref.numpy(), rtol=tol, atol=tol)
+    mixer_out = res["linear_output"] if kind == "linear_attention" else res["attention_output"]
+    np.testing.assert_allclose(mixer_out, mixer.numpy(), rtol=tol, atol=tol)
+    if ffn == "moe":
+        assert res["router_indices"].tolist() == idx.tolist()
+    else:
+        assert res["router_indices"] is None
+
+
+def test_decode_layer_wiring_mistakes_are_caught():
+    """The float64 composition separates the plausible wiring mistakes: the
+    residual added after the FFN instead of before it, the projection
+    skipped, and the mixer output dropped."""
+    pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    x, moe, dense, lin, attn = _layer_inputs(seed=4)
+    ref, _, mixer = _decode_layer64(x, "linear_attention", dense=dense, lin=lin)
+    h = t64(x)
+    xn = F.rms_norm(h, (h.shape[1],), weight=t64(dense["norm_weight"]), eps=1e-6)
+    late_residual = h + mixer + _swiglu64(xn, t64(dense["gate_weight"]), t64(dense["up_weight"]),
+                                          t64(dense["down_weight"]))
+    no_mixer = torch.from_numpy(oracle.dense_ffn_decode(x, *(dense[n] for n in (
+        "norm_weight", "gate_weight", "up_weight", "down_weight")))).double()
+    res = oracle.decode_layer(x, kind="linear_attention", dense_ffn=dense, linear_attention=lin, round_to_bf16=False)
+    np.testing.assert_allclose(res["hidden"], ref.numpy(), rtol=2e-4, atol=2e-4)
+    for wrong in (late_residual, no_mixer):
+        assert not np.allclose(res["hidden"], wrong.numpy(), rtol=1e-2, atol=1e-2)
+
+
+def test_decode_layer_special_cases():
+    x, moe, dense, lin, attn = _layer_inputs(seed=5)
+    x = oracle.bf16_round(x)
+    # zero out_proj: the mixer adds nothing, so the layer is the MoE of its input
+    lin0 = dict(lin, out_proj=np.zeros_like(lin["out_proj"]))
+    res = oracle.decode_layer(x, kind="linear_attention", moe=moe, linear_attention=lin0, top_k=3)
+    out, idx, w = oracle.moe_decode(x, *(moe[n] for n in ("norm_weight", "router_weight", "expert_gate", "expert_up",
+                                                          "expert_down", "shared_gate", "shared_up", "shared_down")),
+                                    top_k=3, shared_expert_gate=moe["shared_expert_gate"])
+    np.testing.assert_array_equal(res["hidden"], out)
+    assert res["router_indices"].tolist() == idx.tolist()
+    np.testing.assert_array_equal(res["router_weights"], w)
+    # zero-gate dense FFN: the FFN adds nothing, so hidden = round(x + mixer output)
+    d0 = dict(dense, gate_weight=np.zeros_like(dense["gate_weight"]))
+    res = oracle.decode_layer(x, kind="full_attention", dense_ffn=d0, full_attention=attn)
+    np.testing.assert_array_equal(res["hidden"], oracle.bf16_round(x + res["attention_output"]))
+    # the state of the linear layer is the gated delta rule's
+    res = oracle.decode_layer(x, kind="linear_attention", dense_ffn=dense, linear_attention=lin)
+    _, s = oracle.gated_delta_decode(lin["q"], lin["k"], lin["v"], lin["state"], lin["g"], lin["beta"])
+    np.testing.assert_array_equal(res["linear_state"], s)
+    # without out_proj the output is reshaped onto the hidden size (8 heads x 4 = 32 = H)
+    attn_r = dict(q=randn(2, 8, 4), k_cache=randn(2, 5, 2, 4), v_cache=randn(2, 5, 2, 4))
+    res = oracle.decode_layer(x, kind="full_attention", dense_ffn=d0, full_attention=attn_r)
+    a = oracle.bf16_round(oracle.full_attention_decode(attn_r["q"], attn_r["k_cache"], attn_r["v_cache"]))
+    np.testing.assert_array_equal(res["attention_output"], a.reshape(x.shape))
+    # qk_l2norm and q_scale reach the recurrence
+    lin_n = dict(lin, q=lin["q"] * 3.0, qk_l2norm=True, q_scale=0.25)
+    res = oracle.decode_layer(x, kind="linear_attention", dense_ffn=dense, linear_attention=lin_n)
+    o, s = oracle.gated_delta_decode(lin_n["q"], lin["k"], lin["v"], lin["state"], lin["g"], lin["beta"],
+                                     qk_l2norm=True, q_scale=0.25)
+    np.testing.assert_array_equal(res["linear_state"], s)
+    # KV append through decode_layer reads the new row
+    kn, vn = randn(2, 2, 8), randn(2, 2, 8)
+    res = oracle.decode_layer(x, kind="full_attention", dense_ffn=d0,
+                              full_attention=dict(attn, k_new=kn, v_new=vn, cache_seqlen=4))
+    kc = attn["k_cache"].copy()
+    vc = attn["v_cache"].copy()
+    kc[:, 4], vc[:, 4] = kn, vn
+    a = oracle.bf16_round(oracle.full_attention_decode(attn["q"], kc[:, :5], vc[:, :5], scale=attn["scale"]))
+    a = oracle.bf16_round(a.reshape(2, -1) @ attn["out_proj"].T)
+    np.testing.assert_array_equal(res["attention_output"], a)
+
+
+def test_decode_layer_errors_match_ops():
+    """The ValueError texts of ops.py:720-721, 725-726, 730-731, 738-739."""
+    x, moe, dense, lin, attn = _layer_inputs(seed=6)
+    with pytest.raises(ValueError, match="full_attention inputs are required for full_attention layers"):
+        oracle.decode_layer(x, kind="full_attention", moe=moe)
+    with pytest.raises(ValueError, match="linear_attention inputs are required for linear_attention layers"):
+        oracle.decode_layer(x, kind="linear_attention", moe=moe)
+    with pytest.raises(ValueError, match="unsupported layer_type: vision"):
+        oracle.decode_layer(x, kind="vision", moe=moe)
+    with pytest.raises(ValueError, match="either moe or dense_ffn weights are required"):
+        oracle.decode_layer(x, kind="linear_attention", linear_attention=lin)
+    with pytest.raises(ValueError, match="qk_l2norm needs the gated delta rule"):
+        oracle.decode_layer(x, kind="linear_attention", moe=moe,
+                            linear_attention=dict(q=lin["q"], k=lin["k"], v=lin["v"][:, :2], state=lin["state"],
+                                                  qk_l2norm=True))
+
+
 def test_pinning_table_covers_every_function():
-    for name in ("rms_norm", "topk_desc", "moe_decode", "dense_ffn_decode", "apply_partial_rope",
-                 "full_attention_decode", "linear_attention_decode", "gated_delta_decode", "decode_layer"):
-        assert name in oracle.PINNING
+    for name in oracle.decode_oracle.__all__:
+        if name in ("as_f32", "bf16_bits", "bf16_round", "PINNING", "silu", "softmax"):
+            continue
+        assert name in oracle.PINNING, name
