@@ -76,6 +76,25 @@ int mkq_moe_decode(int dtype, const void* x, const void* norm_weight, const void
                    int top_k, float eps, int add_residual, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* Residency and failure.  The workgroups of mkq_moe_decode hand values to
+ * each other while they run, so all of them (one per CU) must be resident at
+ * once; the entry point checks once per device that one workgroup fits on a
+ * CU (else MKQ_ERR_UNSUPPORTED).  The reference gets the same guarantee from
+ * cudaLaunchCooperativeKernel (persistent_moe_decode.cu:749-827).  A kernel
+ * running concurrently on another stream can still hold CUs and delay some
+ * workgroups; every wait is bounded, and a wait that runs out (about 2^21
+ * polls) records error 1 in the workspace instead of hanging.  From then on
+ * every call on that workspace writes NaN outputs (indices 0, weights NaN)
+ * until the workspace is reset: stale tagged words are never read.
+ *
+ * mkq_moe_decode_status reads the workspace's error word into *error_code
+ * (0: no wait has timed out since the last reset; 1: one has) and, with
+ * reset != 0 and a nonzero word, zero-fills the whole workspace.  It
+ * synchronises `stream` and copies to the host, so it must not be called
+ * while the stream is being captured into a graph.  No counterpart in the
+ * reference, whose cooperative launch either runs or fails. */
+int mkq_moe_decode_status(void* workspace, size_t workspace_bytes, int reset, int* error_code, void* stream);
+
 /* ------------------------------------------------------------------------
  * Dense SwiGLU FFN decode: out = down(silu(gate(rms(x))) * up(rms(x))) (+ x).
  * No native counterpart in the reference: replaces the torch composite

@@ -54,6 +54,7 @@ constexpr int kDN = 8;         // down rows issued per wave before the act hand-
 constexpr int kRB = 8;         // output rows per block in the multi-row down phase (kRB * kMaxB == 64 lanes)
 constexpr int kMaxEL = 16;     // router logits per lane (E <= 1024)
 constexpr unsigned kSpinLimit = 1u << 21;
+constexpr int kMaxDevCache = 64;  // devices whose residency check is cached
 
 // Workspace layout (bytes).  The generation and error words live in their own
 // 256-byte lines; the tagged arrays follow, each 256-byte aligned.
@@ -350,7 +351,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   int* uslot = reinterpret_cast<int*>(umask + ulimit);               // [ulimit][MB]
   int* ent_src = uslot + ulimit * MB;                             // [MB*K] act rows of a window
   int* ent_of = ent_src + MB * K;                                 // [ulimit][MB] window entry of (u, b)
-  int* misc = ent_of + ulimit * MB;                               // [0]=U, [1..kWaves] counts, [16] error
+  int* misc = ent_of + ulimit * MB;  // [0]=U, [1..kWaves] counts, [16] error, [17] sticky error at launch
   float* part = reinterpret_cast<float*>(misc + 32);                 // [rows_per_wg][MB] running sums
   int* ent_base = reinterpret_cast<int*>(part + a.rows_per_wg * MB);  // [ulimit + 1] first entry of expert u
 
@@ -388,6 +389,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // one).  Loaded by every thread (no branch) after x, so the norm does not
   // wait for it; the tag is first used after the norm.
   const unsigned gen = __hip_atomic_load(w.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // A wait of an earlier launch on this workspace timed out: its tagged words
+  // and generation can no longer be trusted, so every launch writes NaN and
+  // leaves without publishing anything until the host clears the workspace
+  // (mkq_moe_decode_status with reset).  Taken through LDS after the first
+  // barrier, so the whole workgroup takes the same branch.
+  const unsigned err_at_start = __hip_atomic_load(w.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) misc[17] = int(err_at_start);
   // One-row path: the residual of this wave's output row, fetched now; after
   // the expert weights have streamed through, x is no longer in the L2.
   float x_res = 0.f;
@@ -633,6 +641,15 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       for (int v = 0; v < kWaves; ++v) t += red[v * 2 * MB + MB + tid];
       sgf[tid] = a.wsg != nullptr ? 1.0f / (1.0f + expf(-t)) : 1.0f;
     }
+  }
+  if (misc[17] != 0) {
+    for (int t = tid; t < B * nrows; t += kThreads) a.out[size_t(t / nrows) * H + h0 + t % nrows] = from_f<T>(NAN);
+    if (wg == 0)
+      for (int t = tid; t < B * K; t += kThreads) {
+        a.idx[t] = 0;
+        a.wts[t] = NAN;
+      }
+    return;
   }
   const unsigned tag = gen + 1u;
   if (tid == 0) put_tagged(w.presence + wg, 0.f, tag);
@@ -1241,9 +1258,13 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       seen = __all(ready);
       if (!seen) __builtin_amdgcn_s_sleep(1);
     }
+    // After a timed-out wait the generation is left alone: the error word
+    // keeps every later launch out of the tagged arrays until a reset.
     if (lane == 0) {
-      if (!seen) __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(w.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!seen)
+        __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        __hip_atomic_store(w.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -1311,6 +1332,21 @@ int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
     MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     max_lds_per_block()));
     attr_set[slot] = true;
+  }
+  // The workgroups wait for each other, so all nwg (one per CU) must be
+  // resident at once.  Checked once per (device, instance, LDS size).
+  static size_t resident_ok[kMaxDevCache][8] = {};
+  const int dev = current_device();
+  if (dev < 0 || dev >= kMaxDevCache || resident_ok[dev][slot] != lds) {
+    int per_cu = 0;
+    MKQ_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), kThreads,
+                                                             lds));
+    if (per_cu < 1 || int64_t(per_cu) * ncu < nwg)
+      return set_error(MKQ_ERR_UNSUPPORTED,
+                       "moe_decode: %d workgroups of %d threads and %zu bytes of LDS cannot all be resident "
+                       "(%d per CU, %d CUs)",
+                       nwg, kThreads, lds, per_cu, ncu);
+    if (dev >= 0 && dev < kMaxDevCache) resident_ok[dev][slot] = lds;
   }
   for (int b0 = 0; b0 < batch; b0 += kMaxB) {
     a.B = batch - b0 < kMaxB ? batch - b0 : kMaxB;
@@ -1392,4 +1428,22 @@ extern "C" int mkq_moe_decode(int dtype, const void* x, const void* norm_weight,
     default:
       return set_error(MKQ_ERR_INVALID, "moe_decode: unknown dtype %d", dtype);
   }
+}
+
+extern "C" int mkq_moe_decode_status(void* workspace, size_t workspace_bytes, int reset, int* error_code,
+                                     void* stream) {
+  clear_error();
+  MKQ_REQUIRE(workspace && error_code, "moe_decode_status: null pointer");
+  MKQ_REQUIRE(workspace_bytes >= kOffData, "moe_decode_status: workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  unsigned word = 0;
+  MKQ_HIP_TRY(hipMemcpyAsync(&word, static_cast<unsigned char*>(workspace) + kOffErr, sizeof(word),
+                             hipMemcpyDeviceToHost, s));
+  MKQ_HIP_TRY(hipStreamSynchronize(s));
+  *error_code = int(word);
+  if (reset && word != 0) {
+    MKQ_HIP_TRY(hipMemsetAsync(workspace, 0, workspace_bytes, s));
+    MKQ_HIP_TRY(hipStreamSynchronize(s));
+  }
+  return MKQ_OK;
 }

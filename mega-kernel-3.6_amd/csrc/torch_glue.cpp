@@ -51,8 +51,12 @@ hipStream_t current_stream() { return c10::hip::getCurrentHIPStream().stream(); 
 // first allocated (or grown); entry points do not share one, since another
 // entry point's scratch data would overwrite that state.
 enum class Ws { kMoe, kDense, kAttention, kLinearStep };
-torch::Tensor workspace_for(Ws op, const torch::Tensor& like, size_t bytes) {
+std::map<std::tuple<int, int, hipStream_t>, torch::Tensor>& workspace_cache() {
   static std::map<std::tuple<int, int, hipStream_t>, torch::Tensor> cache;
+  return cache;
+}
+torch::Tensor workspace_for(Ws op, const torch::Tensor& like, size_t bytes) {
+  auto& cache = workspace_cache();
   const auto key = std::make_tuple(static_cast<int>(op), static_cast<int>(like.get_device()), current_stream());
   auto it = cache.find(key);
   if (it != cache.end() && static_cast<size_t>(it->second.numel()) >= bytes) return it->second;
@@ -612,6 +616,22 @@ std::tuple<torch::Tensor, torch::Tensor> gemv_add(torch::Tensor x, torch::Tensor
   return {y, sum};
 }
 
+// Error word of the MoE workspace of the current device and stream (0 if
+// that stream has none yet); with reset, a nonzero word clears the workspace.
+// Synchronises the stream.
+int64_t moe_decode_status(bool reset) {
+  int dev = 0;
+  TORCH_CHECK(hipGetDevice(&dev) == hipSuccess, "moe_decode_status: no current device");
+  auto& cache = workspace_cache();
+  auto it = cache.find(std::make_tuple(static_cast<int>(Ws::kMoe), dev, current_stream()));
+  if (it == cache.end()) return 0;
+  int code = 0;
+  const int rc = mkq_moe_decode_status(it->second.data_ptr(), static_cast<size_t>(it->second.numel()), reset ? 1 : 0,
+                                       &code, current_stream());
+  check_status(rc, "moe_decode_status");
+  return code;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -654,5 +674,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("residual") = pybind11::none());
   m.def("gemv_add", &gemv_add, "(y, residual + y) with y = x w^T (HIP)", pybind11::arg("x"), pybind11::arg("w"),
         pybind11::arg("residual"));
+  m.def("moe_decode_status", &moe_decode_status,
+        "Error word of the current stream's MoE workspace (1: a cross-workgroup wait timed out); synchronises",
+        pybind11::arg("reset") = false);
   m.def("abi_version", &mkq_abi_version);
 }

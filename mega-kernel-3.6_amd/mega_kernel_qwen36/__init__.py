@@ -29,6 +29,7 @@ from .ops import (
     linear_attention_decode,
     linear_attention_step,
     moe_decode,
+    moe_decode_status,
 )
 from ._lib import library_path, load_library
 
@@ -52,6 +53,7 @@ __all__ = [
     "linear_attention_step",
     "load_library",
     "moe_decode",
+    "moe_decode_status",
     "qwen36_27b_config",
     "qwen36_35b_a3b_config",
     "qwen36_layer_type",

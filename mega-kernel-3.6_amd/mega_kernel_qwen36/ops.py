@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import dataclasses
 import math
+import os
 import weakref
 from dataclasses import dataclass
 from typing import Optional, Tuple
@@ -252,8 +253,35 @@ def moe_decode(
     _require_extension("moe_decode", *tensors)
     sg = getattr(weights, "shared_expert_gate", None)
     if sg is not None:
-        return _C.moe_decode_persistent_gated(*tensors, sg, float(eps), int(top_k), bool(add_residual))
-    return _C.moe_decode_persistent(*tensors, float(eps), int(top_k), bool(add_residual))
+        return _check_moe(_C.moe_decode_persistent_gated(*tensors, sg, float(eps), int(top_k), bool(add_residual)))
+    return _check_moe(_C.moe_decode_persistent(*tensors, float(eps), int(top_k), bool(add_residual)))
+
+
+def moe_decode_status(*, reset: bool = False) -> int:
+    """Error word of the persistent MoE on the current device and stream.
+
+    0: no cross-workgroup wait has timed out since the last reset.  1: one
+    has (for example because a kernel on another stream held CUs while the
+    MoE's workgroups waited for each other); that call and every later one on
+    the stream wrote NaN outputs, and they keep doing so until ``reset=True``
+    clears the workspace.  Synchronises the stream, so it is not for use
+    inside graph capture.  Set ``MKQ_MOE_CHECK=1`` to have every
+    ``moe_decode`` call check it and raise (a debugging aid: it synchronises
+    after each call).  No counterpart in the reference, whose cooperative
+    launch either runs or fails at launch.
+    """
+    if _C is None:
+        raise RuntimeError(f"moe_decode_status: the HIP extension is not loaded ({_C_IMPORT_ERROR!r})")
+    return int(_C.moe_decode_status(bool(reset)))
+
+
+def _check_moe(result):
+    if os.environ.get("MKQ_MOE_CHECK", "0") not in ("", "0"):
+        code = moe_decode_status(reset=True)
+        if code:
+            raise RuntimeError(f"moe_decode: a cross-workgroup wait timed out (error word {code}); "
+                               "the outputs are NaN and the workspace has been reset")
+    return result
 
 
 def dense_ffn_decode(

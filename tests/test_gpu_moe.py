@@ -259,3 +259,66 @@ def test_moe_topk_ties_lower_index_first(batch):
     assert ref_idx.tolist() == expect.tolist()
     torch.testing.assert_close(rw, torch.from_numpy(np.asarray(ref_w, np.float32)), atol=1e-5, rtol=1e-4)
     assert_close_out(out, ref)
+
+
+# ---------------------------------------------------------------------------
+# failure reporting: the workspace's error word (a timed-out cross-workgroup
+# wait) is reported, makes every later call write NaN instead of reading stale
+# words, and a reset restores normal calls.  The error is planted by the host;
+# no test makes a wait time out.
+# ---------------------------------------------------------------------------
+
+def _moe_capi(lib, x, w, k, out, idx, rw, ws):
+    from mega_kernel_qwen36 import _lib as L
+    b, h = x.shape
+    e, i, _ = w.expert_gate.shape
+    return lib.mkq_moe_decode(L.MKQ_DTYPE_BF16, x.data_ptr(), w.norm_weight.data_ptr(), w.router_weight.data_ptr(),
+                              w.expert_gate.data_ptr(), w.expert_up.data_ptr(), w.expert_down.data_ptr(),
+                              w.shared_gate.data_ptr(), w.shared_up.data_ptr(), w.shared_down.data_ptr(),
+                              w.shared_expert_gate.data_ptr(), out.data_ptr(), idx.data_ptr(), rw.data_ptr(), b, h, e,
+                              i, w.shared_gate.shape[0], k, 1e-6, 1, ws.data_ptr(), ws.numel(),
+                              torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_moe_error_word_is_sticky_until_reset(batch):
+    import ctypes
+
+    from mega_kernel_qwen36 import _lib as L
+    lib = L.load_library()
+    x, w, k = make_moe(batch=batch, hidden=512, experts=16, intermediate=256, shared_intermediate=256, top_k=4,
+                       seed=30 + batch)
+    nbytes = lib.mkq_moe_decode_workspace_bytes(batch, 512, 16, 256, 256, k)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(x)
+    idx = torch.empty(batch, k, dtype=torch.int64, device="cuda")
+    rw = torch.empty(batch, k, dtype=torch.float32, device="cuda")
+    code = ctypes.c_int(-1)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def status(reset):
+        assert lib.mkq_moe_decode_status(ws.data_ptr(), ws.numel(), reset, ctypes.byref(code), stream) == L.MKQ_OK
+        return code.value
+
+    assert _moe_capi(lib, x, w, k, out, idx, rw, ws) == L.MKQ_OK, lib.mkq_last_error()
+    good = (out.clone(), idx.clone(), rw.clone())
+    assert status(0) == 0
+    ws[256] = 1  # the error word, as a timed-out wait leaves it
+    for _ in range(2):
+        assert _moe_capi(lib, x, w, k, out, idx, rw, ws) == L.MKQ_OK
+        torch.cuda.synchronize()
+        assert torch.isnan(out.float()).all() and torch.isnan(rw).all() and (idx == 0).all()
+    assert status(0) == 1 and status(1) == 1 and status(0) == 0
+    assert int(ws.count_nonzero()) == 0
+    assert _moe_capi(lib, x, w, k, out, idx, rw, ws) == L.MKQ_OK
+    torch.cuda.synchronize()
+    assert torch.equal(out, good[0]) and torch.equal(idx, good[1]) and torch.equal(rw, good[2])
+
+
+def test_moe_decode_status_through_python(monkeypatch):
+    x, w, k = make_moe(batch=1, hidden=512, experts=16, intermediate=256, shared_intermediate=256, top_k=4, seed=35)
+    first = mk.moe_decode(x, w, top_k=k)
+    assert mk.moe_decode_status() == 0
+    monkeypatch.setenv("MKQ_MOE_CHECK", "1")
+    again = mk.moe_decode(x, w, top_k=k)
+    assert torch.equal(first[0], again[0])
