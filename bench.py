@@ -445,51 +445,98 @@ def pmc_workload(mk, inputs, name, launches=10):
 # CPU baseline (oracle = numpy restatement of reference.py, on host cores)
 # ---------------------------------------------------------------------------
 
-def cpu_baseline_moe(inputs, budget_s: float):
-    import numpy as np
-    import torch
-
-    import oracle
-
+def _cpu_threads():
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        return int(max([i.get("num_threads", 1) for i in threadpool_info()] or [1]))
     except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    x, w, k = inputs.make_moe(batch=1, device="cpu")
+        return os.cpu_count() or 1
 
-    def bits(t):
-        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
 
-    args = [bits(x)] + [bits(getattr(w, f)) for f in (
-        "norm_weight", "router_weight", "expert_gate", "expert_up", "expert_down",
-        "shared_gate", "shared_up", "shared_down")]
-    sg = bits(w.shared_expert_gate)
-    oracle.moe_decode(*args, top_k=k, shared_expert_gate=sg)  # warmup
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _bits(t):
+    """bf16 tensor -> numpy uint16 bit patterns (the oracle upcasts them per call)."""
+    import numpy as np
+    import torch
+
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _time_cpu(fn, budget_s):
+    fn()  # warmup
     times = []
     t_end = time.perf_counter() + budget_s
     while time.perf_counter() < t_end or len(times) < 3:
         t0 = time.perf_counter()
-        oracle.moe_decode(*args, top_k=k, shared_expert_gate=sg)
+        fn()
         times.append((time.perf_counter() - t0) * 1e6)
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
-        "value": statistics.median(times),
-        "unit": "us/op",
-        "cores": int(threads),
-        "kind": "port",
-        "sample": f"{len(times)} calls of the numpy oracle moe_decode on config 2 at batch 1 "
-                  f"(bf16 bits upcast per call as reference.py does), median; host {cpu_model}, "
-                  f"os.cpu_count()={os.cpu_count()}",
-    }
+    return statistics.median(times), len(times)
+
+
+def cpu_baselines(inputs, budget_s: float):
+    """reference.py's CPU path, restated in numpy (oracle/, kind "port"), timed
+    on the host cores for each headline op on the same seeded inputs as the
+    GPU figures: config 2 MoE at batch 1 (the `cpu_baseline` of the line),
+    config 1 MoE (FP32, the reference's own CPU case), config 3 dense FFN at
+    batch 1, config 4 attention at T = 32768 and config 5 linear attention at
+    batch 1.  Each op gets a bounded share of `budget_s`; the oracle keeps
+    reference.py's op structure (FP32 upcast of the weights on every call,
+    the Python loop over batch x top-k, the per-q-head attention loop)."""
+    import oracle
+
+    threads, model = _cpu_threads(), _cpu_model()
+    out = {}
+
+    def record(name, fn, share, what):
+        us, n = _time_cpu(fn, budget_s * share)
+        out[name] = {"value": us, "unit": "us/op", "cores": threads, "kind": "port",
+                     "sample": f"{n} calls of the numpy oracle {what}, median; host {model}, "
+                               f"os.cpu_count()={os.cpu_count()}"}
+        log(f"cpu baseline {name}: {us:.0f} us/op ({n} calls, {threads} threads)")
+
+    moe_fields = ("norm_weight", "router_weight", "expert_gate", "expert_up", "expert_down",
+                  "shared_gate", "shared_up", "shared_down")
+    x, w, k = inputs.make_moe(batch=1, device="cpu")
+    args = [_bits(x)] + [_bits(getattr(w, f)) for f in moe_fields]
+    sg = _bits(w.shared_expert_gate)
+    record("moe_b1", lambda: oracle.moe_decode(*args, top_k=k, shared_expert_gate=sg), 0.4,
+           "moe_decode on config 2 at batch 1 (bf16 bits upcast per call as reference.py does)")
+    del x, w, args
+    import torch
+
+    x, w, k = inputs.make_moe(batch=1, hidden=512, experts=8, intermediate=256, shared_intermediate=256, top_k=2,
+                              seed=1, device="cpu", dtype=torch.float32)
+    args1 = [x.numpy()] + [getattr(w, f).numpy() for f in moe_fields]
+    sg1 = w.shared_expert_gate.numpy()
+    record("moe_config1", lambda: oracle.moe_decode(*args1, top_k=k, shared_expert_gate=sg1), 0.1,
+           "moe_decode on config 1 (FP32: H 512, E 8, top-2, I 256)")
+    x, w = inputs.make_dense(batch=1, device="cpu")
+    dargs = [_bits(x)] + [_bits(getattr(w, f)) for f in ("norm_weight", "gate_weight", "up_weight", "down_weight")]
+    del x, w
+    record("dense_b1", lambda: oracle.dense_ffn_decode(*dargs), 0.2,
+           "dense_ffn_decode on config 3 at batch 1 (5120 -> 17408 -> 5120)")
+    del dargs
+    inp = inputs.make_attention(seq_len=32768, device="cpu")
+    q, kc, vc = _bits(inp.q), _bits(inp.k_cache), _bits(inp.v_cache)
+    del inp
+    record("attn_t32768", lambda: oracle.full_attention_decode(q, kc, vc, scale=1.0 / 16), 0.2,
+           "full_attention_decode on config 4 at T = 32768 (24 q / 4 kv heads, D 256)")
+    del q, kc, vc
+    inp = inputs.make_gated_delta(batch=1, device="cpu")
+    largs = (_bits(inp.q), _bits(inp.k), _bits(inp.v), inp.state.numpy(), inp.g.numpy(), inp.beta.numpy())
+    record("linear_b1", lambda: oracle.gated_delta_decode(*largs), 0.1,
+           "gated_delta_decode on config 5 at batch 1 (16 q/k heads, 32 v heads, D 128)")
+    return out
 
 
 def main(argv=None):
@@ -501,7 +548,8 @@ def main(argv=None):
     ap.add_argument("--pmc-workload", choices=("moe", "dense", "attn", "linear", "copy"), default=None,
                     help="run one op (or a 256 MiB copy) 10 times after flushes for a rocprofv3 --pmc pass; no JSON")
     ap.add_argument("--quick", action="store_true", help="batch 1 / 32K only")
-    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
+    ap.add_argument("--cpu-budget", type=float, default=25.0,
+                    help="seconds of CPU-baseline work, shared among the ops")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
                     help="how the 1 GiB cache flush before each cold step touches its buffer")
     args = ap.parse_args(argv)
@@ -545,7 +593,13 @@ def main(argv=None):
     gpu_wall = time.perf_counter() - t_start
 
     head = results.get("moe_b1")
-    cpu = cpu_baseline_moe(inputs, args.cpu_budget) if head is not None and args.cpu_budget > 0 else None
+    cpu_ops = cpu_baselines(inputs, args.cpu_budget) if head is not None and args.cpu_budget > 0 else {}
+    cpu = cpu_ops.get("moe_b1")
+    for name, c in cpu_ops.items():  # each headline op's CPU figure beside its GPU figure
+        gpu_name = {"moe_config1": None}.get(name, name)
+        if gpu_name in results:
+            results[gpu_name]["cpu_baseline_us"] = c["value"]
+            results[gpu_name]["gpu_speedup_vs_cpu"] = c["value"] / results[gpu_name]["median_us"]
     roofline = None
     if head is not None:
         roofline = {
@@ -580,6 +634,7 @@ def main(argv=None):
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baselines": cpu_ops or None,
         "ops": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                 for k, v in results.items()},
         "gpu_wall_s": round(gpu_wall, 2),

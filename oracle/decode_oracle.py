@@ -508,6 +508,7 @@ def decode_layer(
                                  shared_expert_gate=m.get("shared_expert_gate"))
         res["router_indices"] = idx
         res["router_weights"] = w
+    res["residual"] = resid  # the FFN/MoE input: hidden plus the mixer output
     res["hidden"] = out
     return res
 

@@ -38,6 +38,17 @@ def _np_fields(obj, names):
     return {n: np32(getattr(obj, n)) for n in names if getattr(obj, n, None) is not None}
 
 
+def _router_gap(ref, moe_np, k):
+    """Smallest gap between consecutive logits among the top k + 1 of every
+    row, for the oracle's MoE input.  The device's MoE input differs from it
+    by the bf16 roundings upstream (one ulp of the residual sum flips here and
+    there, ~1e-3 on a logit), so a composed layer pins the exact top-k order
+    only where the gaps are wider than that."""
+    xn = oracle.rms_norm(ref["residual"], moe_np["norm_weight"])
+    lg = np.sort(xn @ moe_np["router_weight"].T, axis=-1)[:, ::-1][:, : k + 1]
+    return float(np.min(lg[:, :-1] - lg[:, 1:]))
+
+
 @pytest.mark.parametrize("batch", [1, 8])
 def test_decode_layer_gated_delta_with_moe(batch):
     """Config 5 composed with the config-2 MoE (layer 0 is a linear-attention layer)."""
@@ -50,6 +61,7 @@ def test_decode_layer_gated_delta_with_moe(batch):
         np32(x), kind="linear_attention", moe=_np_fields(w, MOE_FIELDS), top_k=k,
         linear_attention=dict(q=np32(lin.q), k=np32(lin.k), v=np32(lin.v), state=np32(lin.state), g=np32(lin.g),
                               beta=np32(lin.beta), out_proj=np32(lin.out_proj)))
+    assert _router_gap(ref, _np_fields(w, MOE_FIELDS), k) > 1e-3
     assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
     assert_close_out(res.linear_output, ref["linear_output"])
     assert_close_state(res.linear_state, ref["linear_state"])
@@ -83,7 +95,7 @@ def test_decode_layer_attention_append_with_moe(layout):
     """A full-attention layer whose new token is appended inside the attention
     kernel, contiguous or paged (16-token blocks in a shuffled pool), against
     the oracle's decode_layer over the same cache layout."""
-    x, w, k = make_moe(batch=2, seed=200)
+    _, w, k = make_moe(batch=2, seed=200)
     att = make_attention(batch=2, seq_len=1000, seed=201)
     g = torch.Generator().manual_seed(202)
     k_new = torch.randn(2, 4, 256, generator=g).to("cuda", torch.bfloat16)
@@ -100,9 +112,15 @@ def test_decode_layer_attention_append_with_moe(layout):
         fields = dict(k_cache=kp, v_cache=vp, k_new=k_new, v_new=v_new, block_table=perm.to("cuda"), seq_len=977)
     ref_fields = {n: (np32(t) if isinstance(t, torch.Tensor) else t) for n, t in fields.items()}
     att = dataclasses.replace(att, out_proj=proj, **fields)
-    ref = oracle.decode_layer(
-        np32(x), kind="full_attention", moe=_np_fields(w, MOE_FIELDS), top_k=k,
-        full_attention=dict(q=np32(att.q), scale=att.scale, out_proj=np32(proj), **ref_fields))
+    moe_np = _np_fields(w, MOE_FIELDS)
+    for seed in range(210, 230):  # hidden states whose routing has no near-tie (see _router_gap)
+        x = torch.randn(2, 2048, generator=torch.Generator().manual_seed(seed)).to("cuda", torch.bfloat16)
+        ref = oracle.decode_layer(
+            np32(x), kind="full_attention", moe=moe_np, top_k=k,
+            full_attention=dict(q=np32(att.q), scale=att.scale, out_proj=np32(proj), **ref_fields))
+        if _router_gap(ref, moe_np, k) > 3e-3:
+            break
+    assert _router_gap(ref, moe_np, k) > 3e-3
     res = mk.decode_layer(3, x, w, full_attention=att, top_k=k)
     assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
     assert_close_out(res.attention_output, ref["attention_output"])
