@@ -100,7 +100,7 @@ def test_decode_layer_attention_append_with_moe(layout):
     g = torch.Generator().manual_seed(202)
     k_new = torch.randn(2, 4, 256, generator=g).to("cuda", torch.bfloat16)
     v_new = torch.randn(2, 4, 256, generator=g).to("cuda", torch.bfloat16)
-    proj = _proj(x.shape[1], 24 * 256, 203)
+    proj = _proj(w.norm_weight.shape[0], 24 * 256, 203)
     if layout == "append":
         kc, vc = att.k_cache.clone(), att.v_cache.clone()
         fields = dict(k_cache=kc, v_cache=vc, k_new=k_new, v_new=v_new, cache_seqlen=700)
