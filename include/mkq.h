@@ -95,6 +95,29 @@ int mkq_moe_decode(int dtype, const void* x, const void* norm_weight, const void
  * reference, whose cooperative launch either runs or fails. */
 int mkq_moe_decode_status(void* workspace, size_t workspace_bytes, int reset, int* error_code, void* stream);
 
+/* MoE decode that allocates nothing and takes no workspace.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory or
+ * own a workspace (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * mkq_moe_decode, minus (workspace, workspace_bytes): the workspace is a
+ * static device array of MKQ_MOE_NOALLOC_SCRATCH_BYTES in libmkq.so, one per
+ * GPU, zero when the library is loaded and held until the process ends; its
+ * address is looked up once per device.  A shape whose workspace
+ * (mkq_moe_decode_workspace_bytes) exceeds it returns MKQ_ERR_UNSUPPORTED
+ * (config 2 needs about 2.5 MB).  Every call on one GPU shares that array and
+ * leaves its generation word advanced for the next call, so calls that
+ * overlap on one GPU (several streams, several host threads) race and must
+ * be serialised by the caller.  If a wait ever times out (see above), every
+ * later call of this entry point on that GPU writes NaN outputs until the
+ * process ends: mkq_moe_decode_status cannot reach the static array. */
+#define MKQ_MOE_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int mkq_moe_decode_noalloc(int dtype, const void* x, const void* norm_weight, const void* router_weight,
+                           const void* expert_gate, const void* expert_up, const void* expert_down,
+                           const void* shared_gate, const void* shared_up, const void* shared_down,
+                           const void* shared_expert_gate, void* out, int64_t* indices, float* weights,
+                           int batch, int hidden, int experts, int intermediate, int shared_intermediate,
+                           int top_k, float eps, int add_residual, void* stream);
+
 /* ------------------------------------------------------------------------
  * Dense SwiGLU FFN decode: out = down(silu(gate(rms(x))) * up(rms(x))) (+ x).
  * No native counterpart in the reference: replaces the torch composite

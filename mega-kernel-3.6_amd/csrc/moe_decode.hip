@@ -36,6 +36,8 @@
 // several batch rows select it).
 #include <math.h>
 
+#include <mutex>
+
 #include "mkq_host.h"
 
 using namespace mkq;
@@ -1370,29 +1372,20 @@ extern "C" size_t mkq_moe_decode_workspace_bytes(int batch, int hidden, int expe
   return ws_bytes(experts, intermediate, shared_intermediate, top_k);
 }
 
-extern "C" int mkq_moe_decode(int dtype, const void* x, const void* norm_weight, const void* router_weight,
-                              const void* expert_gate, const void* expert_up, const void* expert_down,
-                              const void* shared_gate, const void* shared_up, const void* shared_down,
-                              const void* shared_expert_gate, void* out, int64_t* indices, float* weights, int batch,
-                              int hidden, int experts, int intermediate, int shared_intermediate, int top_k,
-                              float eps, int add_residual, void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  MKQ_REQUIRE(batch > 0 && hidden > 0 && experts > 0 && intermediate > 0 && shared_intermediate > 0,
-              "moe_decode: sizes must be positive");
-  MKQ_REQUIRE(top_k > 0 && top_k <= experts, "top_k must be in [1, experts]");
-  MKQ_REQUIRE(x && norm_weight && router_weight && expert_gate && expert_up && expert_down && shared_gate &&
-                  shared_up && shared_down && out && indices && weights,
-              "moe_decode: null tensor pointer");
+namespace {
+
+// Argument checks and dtype dispatch shared by mkq_moe_decode and
+// mkq_moe_decode_noalloc; `fn` names the entry point in error messages.
+int moe_entry(const char* fn, int dtype, const void* x, const void* norm_weight, const void* router_weight,
+              const void* expert_gate, const void* expert_up, const void* expert_down, const void* shared_gate,
+              const void* shared_up, const void* shared_down, const void* shared_expert_gate, void* out,
+              int64_t* indices, float* weights, int batch, int hidden, int experts, int intermediate,
+              int shared_intermediate, int top_k, float eps, int add_residual, void* workspace,
+              size_t workspace_bytes, void* stream) {
   MKQ_REQUIRE(workspace && workspace_bytes >= mkq_moe_decode_workspace_bytes(batch, hidden, experts, intermediate,
                                                                               shared_intermediate, top_k),
-              "moe_decode: workspace too small");
-  MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "moe_decode: workspace must be 256-byte aligned");
-  if (experts > kMaxEL * kWave || top_k > 64)
-    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: experts <= %d and top_k <= 64 are supported", kMaxEL * kWave);
-  const int epc = dtype == MKQ_DTYPE_F32 ? 4 : 8;
-  const int maxh = epc * kWave * kMaxHC, maxi = epc * kWave * kMaxIC;
-  if (hidden > maxh || intermediate > maxi || shared_intermediate > maxi)
-    return set_error(MKQ_ERR_UNSUPPORTED, "moe_decode: hidden <= %d and intermediate <= %d are supported", maxh, maxi);
+              "%s: workspace too small", fn);
+  MKQ_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "%s: workspace must be 256-byte aligned", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
 #define MKQ_MOE_CASE(CODE, TYPE)                                 \
@@ -1426,8 +1419,104 @@ extern "C" int mkq_moe_decode(int dtype, const void* x, const void* norm_weight,
     MKQ_MOE_CASE(MKQ_DTYPE_F32, float)
 #undef MKQ_MOE_CASE
     default:
-      return set_error(MKQ_ERR_INVALID, "moe_decode: unknown dtype %d", dtype);
+      return set_error(MKQ_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
   }
+}
+
+// Checks that need no workspace: sizes, pointers, supported shapes.
+int moe_check_args(const char* fn, int dtype, const void* x, const void* norm_weight, const void* router_weight,
+                   const void* expert_gate, const void* expert_up, const void* expert_down, const void* shared_gate,
+                   const void* shared_up, const void* shared_down, const void* out, const void* indices,
+                   const void* weights, int batch, int hidden, int experts, int intermediate, int shared_intermediate,
+                   int top_k) {
+  MKQ_REQUIRE(batch > 0 && hidden > 0 && experts > 0 && intermediate > 0 && shared_intermediate > 0,
+              "%s: sizes must be positive", fn);
+  MKQ_REQUIRE(top_k > 0 && top_k <= experts, "top_k must be in [1, experts]");
+  MKQ_REQUIRE(x && norm_weight && router_weight && expert_gate && expert_up && expert_down && shared_gate &&
+                  shared_up && shared_down && out && indices && weights,
+              "%s: null tensor pointer", fn);
+  if (experts > kMaxEL * kWave || top_k > 64)
+    return set_error(MKQ_ERR_UNSUPPORTED, "%s: experts <= %d and top_k <= 64 are supported", fn, kMaxEL * kWave);
+  const int epc = dtype == MKQ_DTYPE_F32 ? 4 : 8;
+  const int maxh = epc * kWave * kMaxHC, maxi = epc * kWave * kMaxIC;
+  if (hidden > maxh || intermediate > maxi || shared_intermediate > maxi)
+    return set_error(MKQ_ERR_UNSUPPORTED, "%s: hidden <= %d and intermediate <= %d are supported", fn, maxh, maxi);
+  return MKQ_OK;
+}
+
+// Scratch of mkq_moe_decode_noalloc: the MoE workspace (generation and error
+// words, tagged logits, act and shared act) as a static device array, one per
+// GPU, held until the process ends.  Device globals start zeroed when the
+// code object is loaded, which is the state a fresh workspace must have; the
+// generation protocol then keeps it valid from call to call, so nothing is
+// cleared per call.  Its address is taken once per device with
+// hipGetSymbolAddress (host code never passes `scratch` itself).
+constexpr size_t kNoAllocScratchBytes = MKQ_MOE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevCache] = {};
+
+// Device address of this device's `scratch`, looked up on first use.
+int scratch_ptr(const char* fn, void** out) {
+  const int dev = current_device();
+  if (dev < 0 || dev >= kMaxDevCache)
+    return set_error(MKQ_ERR_UNSUPPORTED, "%s: device %d is beyond the %d devices supported", fn, dev, kMaxDevCache);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(MKQ_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MKQ_OK;
+}
+
+}  // namespace
+
+extern "C" int mkq_moe_decode(int dtype, const void* x, const void* norm_weight, const void* router_weight,
+                              const void* expert_gate, const void* expert_up, const void* expert_down,
+                              const void* shared_gate, const void* shared_up, const void* shared_down,
+                              const void* shared_expert_gate, void* out, int64_t* indices, float* weights, int batch,
+                              int hidden, int experts, int intermediate, int shared_intermediate, int top_k,
+                              float eps, int add_residual, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* fn = "moe_decode";
+  const int rc = moe_check_args(fn, dtype, x, norm_weight, router_weight, expert_gate, expert_up, expert_down,
+                                shared_gate, shared_up, shared_down, out, indices, weights, batch, hidden, experts,
+                                intermediate, shared_intermediate, top_k);
+  if (rc != MKQ_OK) return rc;
+  return moe_entry(fn, dtype, x, norm_weight, router_weight, expert_gate, expert_up, expert_down, shared_gate,
+                   shared_up, shared_down, shared_expert_gate, out, indices, weights, batch, hidden, experts,
+                   intermediate, shared_intermediate, top_k, eps, add_residual, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mkq_moe_decode_noalloc(int dtype, const void* x, const void* norm_weight, const void* router_weight,
+                                      const void* expert_gate, const void* expert_up, const void* expert_down,
+                                      const void* shared_gate, const void* shared_up, const void* shared_down,
+                                      const void* shared_expert_gate, void* out, int64_t* indices, float* weights,
+                                      int batch, int hidden, int experts, int intermediate, int shared_intermediate,
+                                      int top_k, float eps, int add_residual, void* stream) {
+  clear_error();
+  const char* fn = "moe_decode_noalloc";
+  int rc = moe_check_args(fn, dtype, x, norm_weight, router_weight, expert_gate, expert_up, expert_down, shared_gate,
+                          shared_up, shared_down, out, indices, weights, batch, hidden, experts, intermediate,
+                          shared_intermediate, top_k);
+  if (rc != MKQ_OK) return rc;
+  const size_t need = ws_bytes(experts, intermediate, shared_intermediate, top_k);
+  if (need > kNoAllocScratchBytes)
+    return set_error(MKQ_ERR_UNSUPPORTED,
+                     "%s: this shape needs %zu bytes of scratch; the static scratch array holds %zu "
+                     "(use mkq_moe_decode with a caller workspace)",
+                     fn, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_ptr(fn, &ws);
+  if (rc != MKQ_OK) return rc;
+  return moe_entry(fn, dtype, x, norm_weight, router_weight, expert_gate, expert_up, expert_down, shared_gate,
+                   shared_up, shared_down, shared_expert_gate, out, indices, weights, batch, hidden, experts,
+                   intermediate, shared_intermediate, top_k, eps, add_residual, ws, kNoAllocScratchBytes, stream);
 }
 
 extern "C" int mkq_moe_decode_status(void* workspace, size_t workspace_bytes, int reset, int* error_code,

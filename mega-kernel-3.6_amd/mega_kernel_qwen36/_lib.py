@@ -39,6 +39,11 @@ SIGNATURES = {
          _i, _i, _i, _i, _i, _i, _f, _i, _vp, _sz, _vp],
     ),
     "mkq_moe_decode_status": (_i, [_vp, _sz, _i, ctypes.POINTER(_i), _vp]),
+    "mkq_moe_decode_noalloc": (
+        _i,
+        [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+         _i, _i, _i, _i, _i, _i, _f, _i, _vp],
+    ),
     "mkq_dense_ffn_decode_workspace_bytes": (_sz, [_i, _i, _i]),
     "mkq_dense_ffn_decode": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _i, _vp, _sz, _vp]),
     "mkq_full_attention_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),

@@ -61,6 +61,28 @@ def test_c_abi_rejects_bad_arguments_without_gpu():
     assert b"multiple of k_heads" in lib.mkq_last_error()
 
 
+def test_noalloc_moe_entry_validates_on_the_host_without_gpu():
+    """The no-allocation MoE entry point rejects bad arguments, and shapes
+    whose workspace exceeds its static scratch array, before any HIP call."""
+    lib = _lib.load_library()
+    rc = lib.mkq_moe_decode_noalloc(_lib.MKQ_DTYPE_BF16, *([None] * 13), 1, 16, 4, 8, 8, 5, 1e-6, 1, None)
+    assert rc == _lib.MKQ_ERR_INVALID
+    assert b"top_k must be in [1, experts]" in lib.mkq_last_error()
+    rc = lib.mkq_moe_decode_noalloc(_lib.MKQ_DTYPE_BF16, *([None] * 13), 1, 2048, 256, 512, 512, 8, 1e-6, 1, None)
+    assert rc == _lib.MKQ_ERR_INVALID
+    assert b"moe_decode_noalloc: null tensor pointer" in lib.mkq_last_error()
+    # experts 1024, top-64, intermediate 1024: a 33 MB workspace, beyond the 8 MiB array
+    need = lib.mkq_moe_decode_workspace_bytes(1, 2048, 1024, 1024, 1024, 64)
+    assert need > 8 << 20
+    dummy = [256] * 13  # never dereferenced: the size check comes first
+    rc = lib.mkq_moe_decode_noalloc(_lib.MKQ_DTYPE_BF16, *dummy, 1, 2048, 1024, 1024, 1024, 64, 1e-6, 1, None)
+    assert rc == _lib.MKQ_ERR_UNSUPPORTED
+    msg = lib.mkq_last_error()
+    assert b"needs %d bytes of scratch" % need in msg and b"holds %d" % (8 << 20) in msg
+    # config 2 fits
+    assert lib.mkq_moe_decode_workspace_bytes(8, 2048, 256, 512, 512, 8) <= 8 << 20
+
+
 def test_rope_entry_rejects_unsupported_rotary_dims_without_gpu():
     """The in-kernel RoPE entry point validates on the host and returns
     MKQ_ERR_UNSUPPORTED for rotary dims it cannot rotate in the kernel; the
