@@ -65,6 +65,23 @@ constexpr size_t kOffErr = 256;                       // uint32 error code (1 = 
 constexpr size_t kOffPresence = 512;                  // uint64[kMaxWg] tagged
 constexpr size_t kOffData = kOffPresence + 8 * kMaxWg;
 
+// Phase timestamps, compiled only into profiling builds (-DMKQ_MOE_TRACE):
+// lane 0 of every wave stores the 100 MHz real-time counter at numbered
+// points into trace[(wg * kWaves + wave) * 16 + point], a kernel argument
+// (held in scalar registers, so a mark adds no wait for earlier loads).
+#ifdef MKQ_MOE_TRACE
+#define MOE_MARK(n)                                                                 \
+  do {                                                                              \
+    if (lane == 0 && a.trace != nullptr)                                            \
+      a.trace[(size_t(blockIdx.x) * kWaves + wave) * 16 + (n)] = wall_clock64();    \
+  } while (0)
+uint64_t* g_trace = nullptr;  // host side: the buffer given to mkq_moe_set_trace
+#else
+#define MOE_MARK(n) \
+  do {              \
+  } while (0)
+#endif
+
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -90,6 +107,9 @@ struct MoeArgs {
   int nwg;
   int rows_per_wg;  // output rows per WG in phase 3
   int win_floats;   // act window of the multi-row down phase (floats, a multiple of round_up(I, EPC))
+#ifdef MKQ_MOE_TRACE
+  uint64_t* trace;
+#endif
 };
 
 // Every published array (router logits, act, shared act) is written in
@@ -250,9 +270,11 @@ __device__ bool gather_tagged_pairs(rsrc_t r, int pairs, SrcFn src, float* dst, 
 // experts EL*l .. EL*l + EL-1 (16-byte loads of two tagged words each), sorted
 // in the lane; a round is then one wave-wide max of the lane heads and a
 // ballot for the lowest lane holding it, after which that lane pops its head.
-// Returns false (experts 0) if the wait timed out.
-template <int EL>
-__device__ bool route_row(rsrc_t lr, int E, int K, unsigned tag, int lane, int& my_e, float& my_w) {
+// on_slot(s, my_e) runs right after round s (lane s then holds slot s), so a
+// caller can hand out a slot while the later rounds run.  Returns false
+// (experts 0) if the wait timed out.
+template <int EL, typename OnSlot>
+__device__ bool route_row(rsrc_t lr, int E, int K, unsigned tag, int lane, int& my_e, float& my_w, OnSlot on_slot) {
   u32x4 word[EL / 2];
   bool ok = true;
   for (unsigned polls = 0;;) {
@@ -312,6 +334,7 @@ __device__ bool route_row(rsrc_t lr, int E, int K, unsigned tag, int lane, int& 
       my_e = (best != 0u && e < E) ? e : 0;  // 0 = absent (timed-out wait)
       my_v = ord_value(best);
     }
+    on_slot(s, my_e);
   }
   // Slot 0 holds the largest logit; exp(v_s - v_0) summed in slot order.
   const float first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
@@ -331,6 +354,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = wave_id();
   const int wg = blockIdx.x, nwg = a.nwg;
+  MOE_MARK(0);
   const int B = a.B, H = a.H, E = a.E, I = a.I, Is = a.Is, K = a.K;
   const int Hp = round_up(H, EPC), Ip = round_up(I, EPC), Isp = round_up(Is, EPC);
   const WsPtrs w = ws_ptrs(a.ws, E, I, Is, K);
@@ -353,7 +377,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   int* uslot = reinterpret_cast<int*>(umask + ulimit);               // [ulimit][MB]
   int* ent_src = uslot + ulimit * MB;                             // [MB*K] act rows of a window
   int* ent_of = ent_src + MB * K;                                 // [ulimit][MB] window entry of (u, b)
-  int* misc = ent_of + ulimit * MB;  // [0]=U, [1..kWaves] counts, [16] error, [17] sticky error at launch
+  int* misc = ent_of + ulimit * MB;  // [0]=U, [1..kWaves] counts, [16] error, [17] sticky error at launch,
+                                     // [18] one-row routing progress
   float* part = reinterpret_cast<float*>(misc + 32);                 // [rows_per_wg][MB] running sums
   int* ent_base = reinterpret_cast<int*>(part + a.rows_per_wg * MB);  // [ulimit + 1] first entry of expert u
 
@@ -636,8 +661,12 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       const float t = wave_sum_u(gs[b]);
       if (lane == 0) red[wave * 2 * MB + MB + b] = t;
     }
-    if (tid == 0) misc[16] = 0;
+    if (tid == 0) {
+      misc[16] = 0;
+      misc[18] = 0;  // one-row routing progress (slots handed out)
+    }
     __syncthreads();
+    MOE_MARK(1);
     if (tid < B) {
       float t = 0.f;
       for (int v = 0; v < kWaves; ++v) t += red[v * 2 * MB + MB + tid];
@@ -671,6 +700,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     if (e0 < E) {
       const float s = wave_sum_u(dot_row<T, HC>(rrow, xn, H, lane));
       if (lane < kCopies) put_tagged(w.logits + lane * logit_copy_words(E) + e0, s, tag);
+      MOE_MARK(2);
     }
   } else if (wave < B) {
     for (int e = e0, r = 0; e < E; e += rstep, ++r) {
@@ -719,59 +749,48 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     }
     pin_loads();
     // ---- phases 1-2, one batch row ---------------------------------------------
-    // Wave 0 gathers all logits and routes; the other waves wait at the
-    // barrier below (one polling wave per WG keeps the coherent read traffic
-    // of the exchange 8x lower than every wave polling).  Lane l holds the
-    // logits of experts EL*l .. EL*l + EL-1 (16-byte loads of two tagged
-    // words each), sorted in the lane by (logit descending, index ascending).
-    // A top-k round is then one wave-wide max of the lane heads and a ballot
-    // for the lowest lane holding it -- the lowest expert index among equal
-    // logits, the reference's tie rule -- after which that lane pops its head.
-    // Lane s keeps slot s (expert, logit); the softmax over the K selected
-    // logits is taken once at the end, all slots in parallel.
-    if (wave == 0) {
-      int my_e;
-      float my_w;
-      if (!route_row<EL>(make_rsrc(w.logits + (wg % kCopies) * logit_copy_words(E), uint32_t(E) * 8u), E, K, tag,
-                         lane, my_e, my_w) &&
-          lane == 0)
-        misc[16] = 1;
-      if (lane < K) {
-        sel_e[lane] = my_e;
-        sel_w[lane] = my_w;
-        if (wg == 0) {
-          a.idx[lane] = my_e;
-          a.wts[lane] = my_w;
-        }
-      }
-      if (s0 < Is) issue_shared_gu();
-      issue_shared_down();
-      pin_loads();
-    }
-    __syncthreads();
+    // Wave 0 gathers all logits and routes (one polling wave per WG keeps the
+    // coherent read traffic of the exchange 8x lower than every wave polling;
+    // the top-k rounds are bound by the SIMD's issue rate, so a second
+    // routing wave on a SIMD would slow both).  Lane l holds the logits of
+    // experts EL*l .. EL*l + EL-1 (16-byte loads of two tagged words each),
+    // sorted in the lane by (logit descending, index ascending).  A top-k
+    // round is then one wave-wide max of the lane heads and a ballot for the
+    // lowest lane holding it -- the lowest expert index among equal logits,
+    // the reference's tie rule -- after which that lane pops its head.
+    // After round s wave 0 writes slot s's expert to LDS and advances a
+    // counter there; each wave issues its first group of gate/up rows as soon
+    // as the counter covers the group's slots, while the later rounds run.
+    // The counter reaches K + 1 once the route weights (softmax over the K
+    // selected logits) are in LDS too.
+    int* const ready = misc + 18;
+    // The round after which every slot of this wave's first group is known.
+    const int nw_total = nwg * kWaves;
+    const int gw = wave * nwg + wg;
+    const int ntask = K * I;
+    const int first_ready = min(K - 1, min(gw * kGU + kGU - 1, ntask - 1) / I);
     auto slot_expert = [&](int u) { return __builtin_amdgcn_readfirstlane(sel_e[u]); };
     auto slot_weight = [&](int u) { return sel_w[u]; };
     const size_t hrow = size_t(min(h0 + wave, H - 1));
 
-    // Routed gate/up: task t = (slot t / I, row t % I), t = gw + nw_total * m.
-    const int nw_total = nwg * kWaves;
-    const int gw = wave * nwg + wg;
-    const int ntask = K * I;
-    const int step = nw_total * kGU;
-    auto issue_gu = [&](int t0, u32x4 (&g)[kGU][HC], u32x4 (&u)[kGU][HC]) {
+    // Routed gate/up: tasks t = (slot t / I, row t % I) in groups of kGU
+    // consecutive tasks; wave gw takes groups gw, gw + nw_total, ...  At the
+    // batch-1 shape (K * I = 2 * nwg * kWaves) a wave's one group lies in one
+    // slot: wave w of every WG reads rows of slot w.
+    auto issue_gu = [&](int grp, u32x4 (&g)[kGU][HC], u32x4 (&u)[kGU][HC]) {
 #pragma unroll
       for (int q = 0; q < kGU; ++q) {
-        const int t = t0 + q * nw_total;
+        const int t = grp * kGU + q;
         const int tc = min(t, ntask - 1);
         const size_t ro = (size_t(slot_expert(tc / I)) * I + tc % I) * H;
         load_row<T, VEC, HC>(a.eg + ro, H, t < ntask, lane, g[q]);
         load_row<T, VEC, HC>(a.eu + ro, H, t < ntask, lane, u[q]);
       }
     };
-    auto compute_gu = [&](int t0, const u32x4 (&g)[kGU][HC], const u32x4 (&u)[kGU][HC]) {
+    auto compute_gu = [&](int grp, const u32x4 (&g)[kGU][HC], const u32x4 (&u)[kGU][HC]) {
 #pragma unroll
       for (int q = 0; q < kGU; ++q) {
-        const int t = t0 + q * nw_total;
+        const int t = grp * kGU + q;
         if (t < ntask) {
           const int su = t / I, i = t % I;
           float gv = dot_row<T, HC>(g[q], xn, H, lane);
@@ -782,27 +801,66 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         }
       }
     };
+    // Waits (bounded; wave 0 always gets there) until the counter passes n.
+    auto wait_ready = [&](int n) {
+      for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
+        if (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) > n) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    };
     u32x4 gA[kGU][HC], uA[kGU][HC], gB[kGU][HC], uB[kGU][HC];
-    issue_gu(gw, gA, uA);
-    pin_loads();
+    if (wave == 0) {
+      int my_e;
+      float my_w;
+      const bool routed =
+          route_row<EL>(make_rsrc(w.logits + (wg % kCopies) * logit_copy_words(E), uint32_t(E) * 8u), E, K, tag,
+                        lane, my_e, my_w, [&](int s, int e) {
+                          if (lane == s) sel_e[s] = e;
+                          if (lane == 0) __hip_atomic_store(ready, s + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                          if (s == first_ready) {
+                            issue_gu(gw, gA, uA);
+                            pin_loads();
+                          }
+                        });
+      if (!routed && lane == 0) misc[16] = 1;
+      if (lane < K) sel_w[lane] = my_w;
+      if (lane == 0) __hip_atomic_store(ready, K + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (wg == 0 && lane < K) {
+        a.idx[lane] = my_e;
+        a.wts[lane] = my_w;
+      }
+      if (s0 < Is) issue_shared_gu();
+      issue_shared_down();
+      pin_loads();
+    } else {
+      wait_ready(first_ready);
+      issue_gu(gw, gA, uA);
+      pin_loads();
+    }
+    wait_ready(K);  // route weights in LDS
+    MOE_MARK(3);
     // Shared-expert act of the waves that own a shared row (its rows arrived
     // long ago), before their routed rows: phase 3 needs both.  This code
     // issues no loads (one shared row per wave), so it adds no wait for the
     // gate/up rows just issued.
     publish_shared();
-    for (int t0 = gw; t0 < ntask; t0 += 2 * step) {
-      if (t0 + step < ntask) issue_gu(t0 + step, gB, uB);
+    for (int grp = gw; grp * kGU < ntask; grp += 2 * nw_total) {
+      if ((grp + nw_total) * kGU < ntask) issue_gu(grp + nw_total, gB, uB);
       pin_loads();
-      compute_gu(t0, gA, uA);
-      if (t0 + step >= ntask) break;
-      if (t0 + 2 * step < ntask) issue_gu(t0 + 2 * step, gA, uA);
+      compute_gu(grp, gA, uA);
+      if ((grp + nw_total) * kGU >= ntask) break;
+      if ((grp + 2 * nw_total) * kGU < ntask) issue_gu(grp + 2 * nw_total, gA, uA);
       pin_loads();
-      compute_gu(t0 + step, gB, uB);
+      compute_gu(grp + nw_total, gB, uB);
     }
-    // Down rows of (this wave's output row, expert of slot s) and the shared
-    // down row: needed only after the act exchange, so they are issued once
-    // this wave's gate/up rows are consumed and stream during the exchange
-    // instead of competing with the gate/up rows that the exchange waits for.
+    MOE_MARK(4);
+    // Down rows of (this wave's output row, expert of slot s): needed only
+    // after the act exchange, so they are issued once the whole WG's gate/up
+    // rows are consumed and stream during the exchange.  A CU serves its
+    // loads at a bounded rate, so down rows issued by its early waves would
+    // delay the gate/up rows of its late waves, which the exchange waits for
+    // (-1.8 us at batch 1 with the barrier).
+    __syncthreads();
     u32x4 dn[kDN][IC];
 #pragma unroll
     for (int s = 0; s < kDN; ++s)
@@ -854,6 +912,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     }
     if (!ok3) misc[16] = 1;
     __syncthreads();
+    MOE_MARK(5);
     const bool timed_out = misc[16] != 0;
     if (timed_out && tid == 0) __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Wave w owns output rows h0 + w, h0 + w + kWaves, ...: experts in slot
@@ -895,6 +954,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         a.out[o] = from_f<T>(timed_out ? NAN : s);
       }
     }
+    MOE_MARK(6);
   } else {
 
   // ---- phase 1: gather the router logits, top-k -----------------------------
@@ -905,7 +965,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     float my_w;
     if (!route_row<EL>(make_rsrc(w.logits + (wg % kCopies) * logit_copy_words(E) + size_t(b) * E,
                                  uint32_t(E) * 8u),
-                       E, K, tag, lane, my_e, my_w) &&
+                       E, K, tag, lane, my_e, my_w, [](int, int) {}) &&
         lane == 0) {
       misc[16] = 1;
       __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1269,6 +1329,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         __hip_atomic_store(w.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  MOE_MARK(7);
 }
 
 // LDS floats besides region A (x_norm, later the act window and shared act),
@@ -1286,6 +1347,9 @@ template <typename T>
 int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
   constexpr int EPC = Epc<T>::value;
   MoeArgs<T> a = args0;
+#ifdef MKQ_MOE_TRACE
+  a.trace = g_trace;
+#endif
   const int ncu = cu_count();
   const int nwg = ncu < kMaxWg ? ncu : kMaxWg;
   a.nwg = nwg;
@@ -1318,8 +1382,10 @@ int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
   // The one-row path keeps x_norm, act [K][Ip] and the shared act side by side
   // in the LDS region that the multi-row path shares between them.
   const size_t one_row_floats = Hp + size_t(a.K) * Ip + Isp;
+  // Its routing keeps the E logit keys in the act area until the act gather.
   const bool one_row_ok = batch == 1 && one_row_floats <= max(Hp, win + Isp) &&  // region A as sized for B = 1
-                          a.E <= nwg * kWaves && a.Is <= nwg * kWaves;           // one router / shared row per wave
+                          a.E <= nwg * kWaves && a.Is <= nwg * kWaves &&         // one router / shared row per wave
+                          size_t(a.E) <= size_t(a.K) * Ip + Isp;
   const int which = (vec && hc_need <= 4 && ic_need <= 1) ? (one_row_ok ? 0 : 1) : (vec ? 2 : 3);
   const bool el4 = a.E <= 4 * kWave;
   void (*kern)(MoeArgs<T>) = which == 0   ? (el4 ? &moe_decode_kernel<T, true, 4, 1, 1, 4>
@@ -1363,6 +1429,14 @@ int launch(const MoeArgs<T>& args0, int batch, hipStream_t stream) {
 }
 
 }  // namespace
+
+#ifdef MKQ_MOE_TRACE
+// Profiling builds only: where the kernel stores its phase timestamps.
+extern "C" int mkq_moe_set_trace(void* buf) {
+  g_trace = static_cast<uint64_t*>(buf);
+  return MKQ_OK;
+}
+#endif
 
 extern "C" size_t mkq_moe_decode_workspace_bytes(int batch, int hidden, int experts, int intermediate,
                                                  int shared_intermediate, int top_k) {
