@@ -138,12 +138,15 @@ class Timer:
         }
 
 
-    def pipelined(self, fn, steps: int, cold: bool = True, reps: int = 5):
+    def pipelined(self, fn, steps: int, cold: bool = True, reps: int = 11):
         """Per-op time inside a stream of launches, as a decode loop runs them:
         HIP events around `steps` back-to-back [flush, op] pairs minus `steps`
         back-to-back flushes (cold), or around `steps` back-to-back ops (warm),
         divided by `steps`; median over `reps`.  This leaves out the ~6 us that
-        events around one isolated launch add even for an empty kernel."""
+        events around one isolated launch add even for an empty kernel.  A
+        1 GiB flush takes ~150 us and varies by ~1 % from loop to loop, so one
+        cold repeat carries +-1.5 us of noise per op; the median of 11 repeats
+        keeps the figure within a few tenths of a microsecond."""
         torch = self.torch
         per = []
         for _ in range(reps):

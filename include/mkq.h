@@ -329,6 +329,22 @@ int mkq_gemv(int dtype, const void* x, const void* w, const void* residual, void
 int mkq_gemv_add(int dtype, const void* x, const void* w, const void* residual, void* y, void* sum,
                  int batch, int in_features, int out_features, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Input RMSNorm and projection in one launch:
+ *   xn[b, k] = round(x[b, k] * rsqrt(mean_k(x[b, k]^2) + eps) * norm_weight[k])
+ *   y[b, n]  = round(sum_k w[n, k] * xn[b, k])
+ * (statistics in FP32; round = to the element type, as reference.py:10-13
+ * rounds rms_norm's result).  Replaces the reference planner's task pair
+ * `rmsnorm` -> `linear` (projection "qkv") of a full-attention layer, and the
+ * norm in front of a linear-attention layer's input projection
+ * (mega_kernel_qwen36/mpk_graph.py:349-373, 391-405), which the reference
+ * plans but never executes.  Every workgroup normalises x itself, so there is
+ * no hand-off between workgroups; in_features is limited by staging x
+ * (FP32) in LDS.
+ * ---------------------------------------------------------------------- */
+int mkq_rms_norm_gemv(int dtype, const void* x, const void* norm_weight, float eps, const void* w, void* y,
+                      int batch, int in_features, int out_features, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -616,6 +616,25 @@ std::tuple<torch::Tensor, torch::Tensor> gemv_add(torch::Tensor x, torch::Tensor
   return {y, sum};
 }
 
+torch::Tensor rms_norm_gemv(torch::Tensor x, torch::Tensor norm_weight, torch::Tensor w, double eps) {
+  MK_CHECK_INPUT(x);
+  MK_CHECK_INPUT(norm_weight);
+  MK_CHECK_INPUT(w);
+  TORCH_CHECK(x.dim() == 2, "x must be [batch, in_features]");
+  TORCH_CHECK(w.dim() == 2, "w must be [out_features, in_features]");
+  TORCH_CHECK(w.size(1) == x.size(1), "in_features mismatch");
+  TORCH_CHECK(norm_weight.dim() == 1 && norm_weight.size(0) == x.size(1), "norm_weight must be [in_features]");
+  TORCH_CHECK(x.scalar_type() == w.scalar_type() && x.scalar_type() == norm_weight.scalar_type(),
+              "x, norm_weight and w dtype mismatch");
+  c10::DeviceGuard guard(x.device());
+  auto y = torch::empty({x.size(0), w.size(0)}, x.options());
+  const int rc = mkq_rms_norm_gemv(to_mkq_dtype(x), x.data_ptr(), norm_weight.data_ptr(), static_cast<float>(eps),
+                                   w.data_ptr(), y.data_ptr(), static_cast<int>(x.size(0)),
+                                   static_cast<int>(x.size(1)), static_cast<int>(w.size(0)), current_stream());
+  check_status(rc, "rms_norm_gemv");
+  return y;
+}
+
 // Error word of the MoE workspace of the current device and stream (0 if
 // that stream has none yet); with reset, a nonzero word clears the workspace.
 // Synchronises the stream.
@@ -674,6 +693,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("residual") = pybind11::none());
   m.def("gemv_add", &gemv_add, "(y, residual + y) with y = x w^T (HIP)", pybind11::arg("x"), pybind11::arg("w"),
         pybind11::arg("residual"));
+  m.def("rms_norm_gemv", &rms_norm_gemv, "y = rms_norm(x, norm_weight) w^T, norm rounded to the dtype (HIP)",
+        pybind11::arg("x"), pybind11::arg("norm_weight"), pybind11::arg("w"), pybind11::arg("eps") = 1e-6);
   m.def("moe_decode_status", &moe_decode_status,
         "Error word of the current stream's MoE workspace (1: a cross-workgroup wait timed out); synchronises",
         pybind11::arg("reset") = false);

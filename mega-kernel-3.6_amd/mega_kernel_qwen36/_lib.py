@@ -69,6 +69,7 @@ SIGNATURES = {
                                        _f, _f, _vp, _sz, _vp]),
     "mkq_gemv": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mkq_gemv_add": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "mkq_rms_norm_gemv": (_i, [_i, _vp, _vp, _f, _vp, _vp, _i, _i, _i, _vp]),
 }
 
 

@@ -104,6 +104,13 @@ class FullAttentionInputs:
     # (default max_blocks * block_size).
     block_table: Optional[torch.Tensor] = None
     seq_len: Optional[int] = None
+    # Input projection, used by decode_layer (the reference plans it as the
+    # rmsnorm -> linear "qkv" tasks, mpk_graph.py:349-373): with qkv_proj
+    # [(q_heads + 2*kv_heads)*head_dim, hidden] and input_norm [hidden], q,
+    # k_new and v_new come from rms_norm(hidden) @ qkv_proj^T, in that order,
+    # in one launch, and q may be None.
+    qkv_proj: Optional[torch.Tensor] = None
+    input_norm: Optional[torch.Tensor] = None
 
 
 @dataclass(frozen=True)
@@ -120,6 +127,12 @@ class LinearAttentionInputs:
     # q by q_scale (default 1/sqrt(key_dim)), as use_qk_l2norm_in_kernel does.
     qk_l2norm: bool = False
     q_scale: Optional[float] = None
+    # Input projection, used by decode_layer: with in_proj
+    # [2*k_heads*key_dim + v_heads*value_dim, hidden] and input_norm [hidden],
+    # q, k and v come from rms_norm(hidden) @ in_proj^T (rows [q | k | v]) in
+    # one launch, and q, k, v may be None.
+    in_proj: Optional[torch.Tensor] = None
+    input_norm: Optional[torch.Tensor] = None
 
 
 @dataclass(frozen=True)
@@ -617,6 +630,41 @@ def _project_add(
     return y, summed.reshape_as(hidden)
 
 
+def _project_inputs(hidden: torch.Tensor, norm: torch.Tensor, proj: torch.Tensor, eps: float) -> torch.Tensor:
+    """rms_norm(hidden, norm) @ proj^T in one launch (mkq_rms_norm_gemv)."""
+    _require_extension("decode_layer input projection", hidden, norm, proj)
+    x2 = hidden.reshape(hidden.shape[0], -1).contiguous()
+    return _C.rms_norm_gemv(x2, norm.contiguous(), proj.contiguous(), eps)
+
+
+def _cut(t: torch.Tensor, lo: int, hi: int, *shape: int) -> torch.Tensor:
+    return t[:, lo:hi].reshape(t.shape[0], *shape).contiguous()
+
+
+def _with_projected_qkv(inp: FullAttentionInputs, hidden: torch.Tensor, eps: float) -> FullAttentionInputs:
+    kv_heads, head_dim = inp.k_cache.shape[-2], inp.k_cache.shape[-1]
+    qkv = _project_inputs(hidden, inp.input_norm, inp.qkv_proj, eps)
+    qd = qkv.shape[1] - 2 * kv_heads * head_dim
+    if qd <= 0 or qd % head_dim:
+        raise ValueError("qkv_proj must have (q_heads + 2 * kv_heads) * head_dim rows")
+    kd = kv_heads * head_dim
+    return dataclasses.replace(inp, q=_cut(qkv, 0, qd, qd // head_dim, head_dim),
+                               k_new=_cut(qkv, qd, qd + kd, kv_heads, head_dim),
+                               v_new=_cut(qkv, qd + kd, qd + 2 * kd, kv_heads, head_dim))
+
+
+def _with_projected_qkv_linear(inp: LinearAttentionInputs, hidden: torch.Tensor, eps: float) -> LinearAttentionInputs:
+    _, v_heads, key_dim, value_dim = inp.state.shape
+    qkv = _project_inputs(hidden, inp.input_norm, inp.in_proj, eps)
+    kd = qkv.shape[1] - v_heads * value_dim
+    if kd <= 0 or kd % (2 * key_dim):
+        raise ValueError("in_proj must have 2 * k_heads * key_dim + v_heads * value_dim rows")
+    k_heads = kd // (2 * key_dim)
+    return dataclasses.replace(inp, q=_cut(qkv, 0, kd // 2, k_heads, key_dim),
+                               k=_cut(qkv, kd // 2, kd, k_heads, key_dim),
+                               v=_cut(qkv, kd, qkv.shape[1], v_heads, value_dim))
+
+
 def decode_layer(
     layer_idx: int,
     hidden: torch.Tensor,
@@ -640,10 +688,14 @@ def decode_layer(
     if kind == "full_attention":
         if full_attention is None:
             raise ValueError("full_attention inputs are required for full_attention layers")
+        if full_attention.qkv_proj is not None:
+            full_attention = _with_projected_qkv(full_attention, hidden, eps)
         attention_output, residual = _project_add(full_attention_decode(full_attention), full_attention.out_proj, hidden)
     elif kind == "linear_attention":
         if linear_attention is None:
             raise ValueError("linear_attention inputs are required for linear_attention layers")
+        if linear_attention.in_proj is not None:
+            linear_attention = _with_projected_qkv_linear(linear_attention, hidden, eps)
         linear_output, linear_state = linear_attention_decode(linear_attention)
         linear_output, residual = _project_add(linear_output, linear_attention.out_proj, hidden)
     else:

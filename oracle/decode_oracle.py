@@ -55,6 +55,7 @@ __all__ = [
     "gated_delta_decode",
     "causal_conv1d_update",
     "gated_rms_norm",
+    "rms_norm_linear",
     "attention_cache_view",
     "decode_layer",
     "PINNING",
@@ -108,6 +109,20 @@ def rms_norm(x, weight, eps: float = 1e-6) -> np.ndarray:
     var = np.mean(xf * xf, axis=-1, keepdims=True, dtype=np.float32)
     inv = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
     return (xf * inv * as_f32(weight)).astype(np.float32)
+
+
+def rms_norm_linear(x, norm_weight, w, eps: float = 1e-6, *, round_to_bf16: bool = True) -> np.ndarray:
+    """An input RMSNorm then a projection: ``rms_norm(x).to(dtype) @ w^T``.
+
+    This is the reference planner's ``rmsnorm`` -> ``linear`` task pair in
+    front of a layer's mixer (mega_kernel_qwen36/mpk_graph.py:349-373), with
+    the norm of reference.py:10-13, whose ``.to(x.dtype)`` rounds x_norm to
+    bf16 before the matmul.  With ``round_to_bf16`` x_norm and the product are
+    rounded to bfloat16, as on the bf16 device path; x [B, K], w [N, K].
+    """
+    rnd = bf16_round if round_to_bf16 else (lambda a: as_f32(a))
+    xn = rnd(rms_norm(x, norm_weight, eps))
+    return rnd(xn @ as_f32(w).T)
 
 
 def silu(a: np.ndarray) -> np.ndarray:
@@ -465,7 +480,19 @@ def decode_layer(
     if kind == "full_attention":
         if full_attention is None:
             raise ValueError("full_attention inputs are required for full_attention layers")
-        fa = full_attention
+        fa = dict(full_attention)
+        if fa.get("qkv_proj") is not None:
+            # q, then the new token's key and value, from the layer input
+            kv_h, hd = np.shape(fa["k_cache"])[-2], np.shape(fa["k_cache"])[-1]
+            qkv = rms_norm_linear(h.reshape(h.shape[0], -1), fa["input_norm"], fa["qkv_proj"], eps,
+                                  round_to_bf16=round_to_bf16)
+            qd = qkv.shape[1] - 2 * kv_h * hd
+            if qd <= 0 or qd % hd:
+                raise ValueError("qkv_proj must have (q_heads + 2 * kv_heads) * head_dim rows")
+            b = qkv.shape[0]
+            fa["q"] = qkv[:, :qd].reshape(b, qd // hd, hd)
+            fa["k_new"] = qkv[:, qd:qd + kv_h * hd].reshape(b, kv_h, hd)
+            fa["v_new"] = qkv[:, qd + kv_h * hd:].reshape(b, kv_h, hd)
         k_cache, v_cache = attention_cache_view(fa)
         q, kc = apply_partial_rope(fa["q"], k_cache, fa.get("cos"), fa.get("sin"), fa.get("rotary_dim", 64))
         a = rnd(full_attention_decode(q, kc, v_cache, scale=fa.get("scale")))
@@ -477,7 +504,19 @@ def decode_layer(
     elif kind == "linear_attention":
         if linear_attention is None:
             raise ValueError("linear_attention inputs are required for linear_attention layers")
-        la = linear_attention
+        la = dict(linear_attention)
+        if la.get("in_proj") is not None:
+            # q, k and v from the layer input: rows [q | k | v] of in_proj
+            _, hv, dk, dv = np.shape(la["state"])
+            qkv = rms_norm_linear(h.reshape(h.shape[0], -1), la["input_norm"], la["in_proj"], eps,
+                                  round_to_bf16=round_to_bf16)
+            kd = qkv.shape[1] - hv * dv
+            if kd <= 0 or kd % (2 * dk):
+                raise ValueError("in_proj must have 2 * k_heads * key_dim + v_heads * value_dim rows")
+            b, hk = qkv.shape[0], kd // (2 * dk)
+            la["q"] = qkv[:, :hk * dk].reshape(b, hk, dk)
+            la["k"] = qkv[:, hk * dk:kd].reshape(b, hk, dk)
+            la["v"] = qkv[:, kd:].reshape(b, hv, dv)
         if la.get("g") is not None:
             o, s = gated_delta_decode(la["q"], la["k"], la["v"], la["state"], la["g"], la["beta"],
                                       qk_l2norm=bool(la.get("qk_l2norm", False)), q_scale=la.get("q_scale"))
@@ -535,6 +574,8 @@ PINNING = {
     "attention_cache_view": "append: the written row reads back and every other row is untouched; paged: "
                             "a shuffled pool of blocks gathers back to the contiguous cache it was cut from, "
                             "out-of-pool ids read as zeros",
+    "rms_norm_linear": "float64 torch F.linear(F.rms_norm(x).to(bf16)) composition; identity projection => "
+                       "the rounded norm itself; a scaled input gives the same output (scale invariance of the norm)",
     "decode_layer": "float64 torch composition of ops.py:701-748 (library attention, transformers' gated "
                     "delta loop, float64 SwiGLU/MoE) with and without bf16 rounding between ops; zero out_proj "
                     "=> MoE of the input; zero-gate dense FFN => round(hidden + mixer output); the reshape "

@@ -245,3 +245,110 @@ def test_decode_layer_projected_residual_equals_separate_add():
     assert torch.equal(res.linear_output, y)
     assert torch.equal(res.router_indices, idx)
     assert torch.equal(res.hidden, hidden)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,dtype,kdim,n", [(1, torch.bfloat16, 2048, 8192), (3, torch.bfloat16, 5120, 512),
+                                                (5, torch.float16, 1000, 300), (2, torch.float32, 777, 65)])
+def test_rms_norm_gemv_matches_oracle(batch, dtype, kdim, n):
+    """mkq_rms_norm_gemv (input RMSNorm and projection in one launch) against
+    the oracle's rms_norm_linear: bf16/f16 round the norm and the product to
+    the dtype as the reference's rms_norm does; f32 keeps both.  Batch 5 takes
+    two launches; in_features 1000 / 777 take the element-wise path."""
+    g = torch.Generator().manual_seed(500 + batch)
+    x = torch.randn(batch, kdim, generator=g).to("cuda", dtype)
+    nw = (1 + 0.02 * torch.randn(kdim, generator=g)).to("cuda", dtype)
+    w = (torch.randn(n, kdim, generator=g) * 0.02).to("cuda", dtype)
+    print(f"rms_norm_gemv: batch {batch}, {dtype}, {kdim} -> {n}", flush=True)
+    y = mk.ops._C.rms_norm_gemv(x, nw, w, 1e-6)
+    torch.cuda.synchronize()
+    ref = oracle.rms_norm_linear(np32(x), np32(nw), np32(w), 1e-6, round_to_bf16=dtype == torch.bfloat16)
+    if dtype == torch.float16:
+        ref = (torch.from_numpy(oracle.rms_norm(np32(x), np32(nw))).half().float().numpy() @ np32(w).T)
+    assert_close_out(y, ref)
+    # through the C ABI, same result bit for bit
+    lib = _lib.load_library()
+    y2 = torch.empty_like(y)
+    code = {torch.bfloat16: _lib.MKQ_DTYPE_BF16, torch.float16: _lib.MKQ_DTYPE_F16,
+            torch.float32: _lib.MKQ_DTYPE_F32}[dtype]
+    rc = lib.mkq_rms_norm_gemv(code, x.data_ptr(), nw.data_ptr(), 1e-6, w.data_ptr(), y2.data_ptr(), batch, kdim, n,
+                               torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.MKQ_OK, lib.mkq_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layout", ["append", "paged_append"])
+def test_decode_layer_projects_qkv_with_moe(layout):
+    """A full-attention layer from its pre-norm input: q, k_new and v_new come
+    from rms_norm(hidden) @ qkv_proj^T (config-4 heads, hidden 2048), the new
+    token is appended into the cache inside the attention kernel, then out_proj,
+    the residual and the config-2 MoE; against the oracle's decode_layer with
+    the same projection."""
+    _, w, k = make_moe(batch=2, seed=600)
+    att = make_attention(batch=2, seq_len=1000, seed=601)
+    g = torch.Generator().manual_seed(602)
+    H = w.norm_weight.shape[0]
+    qkv_proj = (torch.randn((24 + 8) * 256, H, generator=g) * 0.02).to("cuda", torch.bfloat16)
+    in_norm = (1 + 0.02 * torch.randn(H, generator=g)).to("cuda", torch.bfloat16)
+    proj = _proj(H, 24 * 256, 603)
+    if layout == "append":
+        fields = dict(k_cache=att.k_cache.clone(), v_cache=att.v_cache.clone(), cache_seqlen=700)
+    else:
+        bs, nb = 16, (1000 + 15) // 16
+        perm = torch.randperm(4 * nb, generator=g)[: 2 * nb].reshape(2, nb).to(torch.int32)
+        kp = torch.randn(4 * nb, bs, 4, 256, generator=g).to("cuda", torch.bfloat16)
+        vp = torch.randn(4 * nb, bs, 4, 256, generator=g).to("cuda", torch.bfloat16)
+        fields = dict(k_cache=kp, v_cache=vp, block_table=perm.to("cuda"), seq_len=977)
+    ref_fields = {n: (np32(t) if isinstance(t, torch.Tensor) else t) for n, t in fields.items()}
+    att = dataclasses.replace(att, q=None, out_proj=proj, qkv_proj=qkv_proj, input_norm=in_norm, **fields)
+    moe_np = _np_fields(w, MOE_FIELDS)
+    for seed in range(610, 640):  # hidden states whose routing has no near-tie (see _router_gap)
+        x = torch.randn(2, H, generator=torch.Generator().manual_seed(seed)).to("cuda", torch.bfloat16)
+        ref = oracle.decode_layer(
+            np32(x), kind="full_attention", moe=moe_np, top_k=k,
+            full_attention=dict(scale=att.scale, out_proj=np32(proj), qkv_proj=np32(qkv_proj),
+                                input_norm=np32(in_norm), **ref_fields))
+        if _router_gap(ref, moe_np, k) > 3e-3:
+            break
+    assert _router_gap(ref, moe_np, k) > 3e-3
+    print(f"decode_layer qkv projection: {layout}, seed {seed}", flush=True)
+    res = mk.decode_layer(3, x, w, full_attention=att, top_k=k)
+    assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
+    assert_close_out(res.attention_output, ref["attention_output"])
+    assert_close_out(res.hidden, ref["hidden"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch", [1, 8])
+def test_decode_layer_projects_linear_inputs_with_moe(batch):
+    """A linear-attention layer from its pre-norm input: q, k and v (config 5:
+    16 q/k heads and 32 v heads of 128) come from rms_norm(hidden) @ in_proj^T,
+    then the gated delta rule with the in-kernel q/k L2 norm, out_proj, the
+    residual and the config-2 MoE; against the oracle's decode_layer."""
+    _, w, k = make_moe(batch=batch, seed=650 + batch)
+    lin = make_gated_delta(batch=batch, seed=660 + batch)
+    g = torch.Generator().manual_seed(670 + batch)
+    H = w.norm_weight.shape[0]
+    in_proj = (torch.randn(2 * 16 * 128 + 32 * 128, H, generator=g) * 0.02).to("cuda", torch.bfloat16)
+    in_norm = (1 + 0.02 * torch.randn(H, generator=g)).to("cuda", torch.bfloat16)
+    lin = dataclasses.replace(lin, q=None, k=None, v=None, in_proj=in_proj, input_norm=in_norm, qk_l2norm=True,
+                              out_proj=_proj(H, 32 * 128, 680 + batch))
+    moe_np = _np_fields(w, MOE_FIELDS)
+    for seed in range(690, 720):
+        x = torch.randn(batch, H, generator=torch.Generator().manual_seed(seed)).to("cuda", torch.bfloat16)
+        ref = oracle.decode_layer(
+            np32(x), kind="linear_attention", moe=moe_np, top_k=k,
+            linear_attention=dict(state=np32(lin.state), g=np32(lin.g), beta=np32(lin.beta),
+                                  out_proj=np32(lin.out_proj), in_proj=np32(in_proj), input_norm=np32(in_norm),
+                                  qk_l2norm=True))
+        if _router_gap(ref, moe_np, k) > 3e-3:
+            break
+    assert _router_gap(ref, moe_np, k) > 3e-3
+    print(f"decode_layer linear in_proj: batch {batch}, seed {seed}", flush=True)
+    res = mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)
+    assert res.router_indices.cpu().tolist() == ref["router_indices"].tolist()
+    assert_close_state(res.linear_state, ref["linear_state"])
+    assert_close_out(res.linear_output, ref["linear_output"])
+    assert_close_out(res.hidden, ref["hidden"])

@@ -83,6 +83,26 @@ def test_noalloc_moe_entry_validates_on_the_host_without_gpu():
     assert lib.mkq_moe_decode_workspace_bytes(8, 2048, 256, 512, 512, 8) <= 8 << 20
 
 
+def test_rms_norm_gemv_entry_validates_on_the_host_without_gpu():
+    lib = _lib.load_library()
+    rc = lib.mkq_rms_norm_gemv(_lib.MKQ_DTYPE_BF16, None, None, 1e-6, None, None, 0, 16, 16, None)
+    assert rc == _lib.MKQ_ERR_INVALID and b"sizes must be positive" in lib.mkq_last_error()
+    rc = lib.mkq_rms_norm_gemv(_lib.MKQ_DTYPE_BF16, 256, None, 1e-6, 256, 256, 1, 16, 16, None)
+    assert rc == _lib.MKQ_ERR_INVALID and b"rms_norm_gemv: null tensor pointer" in lib.mkq_last_error()
+    rc = lib.mkq_rms_norm_gemv(_lib.MKQ_DTYPE_BF16, 256, 256, -1.0, 256, 256, 1, 16, 16, None)
+    assert rc == _lib.MKQ_ERR_INVALID and b"eps must be non-negative" in lib.mkq_last_error()
+
+
+def test_decode_layer_projection_shape_errors_before_device_work():
+    """A qkv_proj / in_proj whose row count does not split into the heads is a
+    ValueError; on CPU tensors the HIP path refuses before any device work."""
+    x = torch.zeros(1, 32, dtype=torch.bfloat16)
+    att = mk.FullAttentionInputs(q=None, k_cache=torch.zeros(1, 4, 2, 8), v_cache=torch.zeros(1, 4, 2, 8),
+                                 qkv_proj=torch.zeros(30, 32), input_norm=torch.ones(32))
+    with pytest.raises(RuntimeError, match="decode_layer input projection"):
+        mk.decode_layer(3, x, None, full_attention=att)
+
+
 def test_rope_entry_rejects_unsupported_rotary_dims_without_gpu():
     """The in-kernel RoPE entry point validates on the host and returns
     MKQ_ERR_UNSUPPORTED for rotary dims it cannot rotate in the kernel; the

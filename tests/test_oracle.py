@@ -681,6 +681,72 @@ def test_decode_layer_errors_match_ops():
                                                   qk_l2norm=True))
 
 
+def test_rms_norm_linear_matches_float64_torch():
+    """rms_norm_linear against F.linear(F.rms_norm(x).to(bf16)) in float64
+    torch (the reference's rms_norm rounds its result to the input dtype,
+    reference.py:10-13), unrounded and rounded; an identity projection gives
+    the (rounded) norm itself; scaling x leaves the output unchanged."""
+    r = np.random.default_rng(11)
+    x = r.standard_normal((3, 48)).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(48)).astype(np.float32)
+    w = (0.2 * r.standard_normal((20, 48))).astype(np.float32)
+    xn64 = F.rms_norm(t64(x), (48,), weight=t64(nw), eps=1e-6)
+    np.testing.assert_allclose(oracle.rms_norm_linear(x, nw, w, round_to_bf16=False),
+                               F.linear(xn64, t64(w)).numpy(), rtol=1e-5, atol=1e-5)
+    ref_b = F.linear(xn64.to(torch.bfloat16).double(), t64(w)).to(torch.bfloat16).double()
+    np.testing.assert_allclose(oracle.rms_norm_linear(x, nw, w), ref_b.numpy(), rtol=1e-2, atol=1e-2)
+    eye = np.eye(48, dtype=np.float32)
+    np.testing.assert_array_equal(oracle.rms_norm_linear(x, nw, eye), oracle.bf16_round(oracle.rms_norm(x, nw)))
+    np.testing.assert_allclose(oracle.rms_norm_linear(4.0 * x, nw, w, round_to_bf16=False),
+                               oracle.rms_norm_linear(x, nw, w, round_to_bf16=False), rtol=1e-5, atol=1e-5)
+    # a dropped norm weight or a transposed projection fails
+    assert not np.allclose(oracle.rms_norm_linear(x, np.ones_like(nw), w), ref_b.numpy(), rtol=1e-2, atol=1e-2)
+
+
+def test_decode_layer_projects_its_own_inputs():
+    """With qkv_proj / in_proj, decode_layer computes the mixer's inputs from
+    the layer input: a full-attention layer equals the layer given q, k_new
+    and v_new cut from rms_norm(hidden) @ qkv_proj^T (in that order), and a
+    linear layer equals the layer given q, k, v cut the same way; both
+    against an independent float64 torch composition of the cuts too."""
+    pytest.importorskip("transformers.models.qwen3_next.modeling_qwen3_next")
+    x, moe, dense, lin, attn = _layer_inputs(seed=8)
+    x = oracle.bf16_round(x)
+    r = np.random.default_rng(12)
+    nw = (1 + 0.1 * r.standard_normal(32)).astype(np.float32)
+    # full attention: 8 q heads and 2 kv heads of 8 -> 96 rows
+    wqkv = (0.3 * r.standard_normal((96, 32))).astype(np.float32)
+    a_in = dict(attn, q=None, qkv_proj=wqkv, input_norm=nw, cache_seqlen=6)
+    res = oracle.decode_layer(x, kind="full_attention", dense_ffn=dense, full_attention=a_in)
+    qkv = oracle.rms_norm_linear(x, nw, wqkv)
+    cut = dict(attn, q=qkv[:, :64].reshape(2, 8, 8), k_new=qkv[:, 64:80].reshape(2, 2, 8),
+               v_new=qkv[:, 80:].reshape(2, 2, 8), cache_seqlen=6)
+    want = oracle.decode_layer(x, kind="full_attention", dense_ffn=dense, full_attention=cut)
+    np.testing.assert_array_equal(res["hidden"], want["hidden"])
+    np.testing.assert_array_equal(res["attention_output"], want["attention_output"])
+    xn = F.rms_norm(t64(x), (32,), weight=t64(nw), eps=1e-6).to(torch.bfloat16).double()
+    qkv64 = F.linear(xn, t64(wqkv)).to(torch.bfloat16).double()
+    np.testing.assert_allclose(qkv, qkv64.numpy(), rtol=1e-2, atol=1e-2)
+    swapped = dict(cut, k_new=cut["v_new"], v_new=cut["k_new"])
+    wrong = oracle.decode_layer(x, kind="full_attention", dense_ffn=dense, full_attention=swapped)
+    assert not np.allclose(res["attention_output"], wrong["attention_output"], rtol=1e-2, atol=1e-2)
+    # linear attention: 2 k heads of 8 (q, k) and 4 v heads of 16 -> 96 rows
+    win = (0.3 * r.standard_normal((96, 32))).astype(np.float32)
+    l_in = dict(lin, q=None, k=None, v=None, in_proj=win, input_norm=nw, qk_l2norm=True)
+    res = oracle.decode_layer(x, kind="linear_attention", moe=moe, linear_attention=l_in, top_k=3)
+    qkv = oracle.rms_norm_linear(x, nw, win)
+    cut = dict(lin, q=qkv[:, :16].reshape(2, 2, 8), k=qkv[:, 16:32].reshape(2, 2, 8),
+               v=qkv[:, 32:].reshape(2, 4, 16), qk_l2norm=True)
+    want = oracle.decode_layer(x, kind="linear_attention", moe=moe, linear_attention=cut, top_k=3)
+    np.testing.assert_array_equal(res["hidden"], want["hidden"])
+    np.testing.assert_array_equal(res["linear_state"], want["linear_state"])
+    with pytest.raises(ValueError, match="qkv_proj must have"):
+        oracle.decode_layer(x, kind="full_attention", dense_ffn=dense,
+                            full_attention=dict(a_in, qkv_proj=wqkv[:30]))
+    with pytest.raises(ValueError, match="in_proj must have"):
+        oracle.decode_layer(x, kind="linear_attention", moe=moe, linear_attention=dict(l_in, in_proj=win[:70]))
+
+
 def test_pinning_table_covers_every_function():
     for name in oracle.decode_oracle.__all__:
         if name in ("as_f32", "bf16_bits", "bf16_round", "PINNING", "silu", "softmax"):
