@@ -15,22 +15,52 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxNb = 4;
-constexpr int kUnroll = 4;
 
-template <typename T, int NB, bool VEC>
+// Work items are (row, segment): a segment is up to 64 * CPL 16-byte chunks of
+// a weight row, loaded as CPL chunks per lane through one buffer descriptor
+// sized to the segment (chunks past it read as zero, with no branch), so all
+// of an item's loads are in flight at once.  Each wave keeps two items in
+// flight; the first two are issued before x is staged.  Segment partial sums
+// meet in LDS and one thread per (batch row, output row) finishes, in a fixed
+// order.
+template <typename T, int NB, int CPL>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x, const T* __restrict__ w,
                                                         const T* __restrict__ residual, T* __restrict__ y,
                                                         T* __restrict__ sum, const T* __restrict__ nw, float eps,
                                                         int kdim, int n, int rows_per_wg) {
   constexpr int EPC = Epc<T>::value;
-  extern __shared__ float xs[];  // [NB][kp], then the norm's partial sums [kWaves][NB]
+  constexpr int kSeg = kWave * CPL;  // chunks per segment
+  extern __shared__ float smem[];    // x [NB][kp], norm partials [kWaves][NB], item sums [items][NB]
   const int kp = (kdim + EPC - 1) / EPC * EPC;
+  const int nch = kp / EPC;
+  const int nseg = (nch + kSeg - 1) / kSeg;
+  float* xs = smem;
   float* red = xs + NB * kp;
-  const int lane = threadIdx.x % kWave, wave = wave_id();
+  float* part = red + kWaves * NB;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int nr = max(0, min(rows_per_wg, n - r0));
+  const int nitems = nr * nseg;
+
+  auto issue = [&](int item, u32x4 (&c)[CPL]) {
+    const bool ok = item < nitems;
+    const int it = ok ? item : 0;
+    const int row = r0 + it / nseg, c0 = (it % nseg) * kSeg;
+    const uint32_t bytes = ok ? uint32_t(min(kSeg, nch - c0)) * 16u : 0u;
+    const rsrc_t rs = make_rsrc(w + size_t(row) * kdim + size_t(c0) * EPC, bytes);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) c[j] = buf_load16<kAuxStream>(rs, uint32_t(lane + kWave * j) * 16u);
+  };
+  u32x4 ca[CPL], cb[CPL];
+  issue(wave, ca);
+  issue(wave + kWaves, cb);
+  pin_loads();
+
+  // x -> LDS (FP32), with its sum of squares for the optional norm.
   float ss[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) ss[b] = 0.f;
-  for (int i = threadIdx.x; i < kp; i += kThreads)
+  for (int i = tid; i < kp; i += kThreads)
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const float v = i < kdim ? to_f(x[size_t(b) * kdim + i]) : 0.f;
@@ -54,77 +84,190 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x,
       for (int v = 0; v < kWaves; ++v) t += red[v * NB + b];
       inv[b] = 1.0f / sqrtf(t / float(kdim) + eps);
     }
-    for (int i = threadIdx.x; i < kdim; i += kThreads) {
+    for (int i = tid; i < kdim; i += kThreads) {
       const float g = to_f(nw[i]);
 #pragma unroll
       for (int b = 0; b < NB; ++b) xs[b * kp + i] = to_f(from_f<T>(xs[b * kp + i] * inv[b] * g));
     }
   }
   __syncthreads();
-  const int nch = kp / EPC;
-  const int r0 = blockIdx.x * rows_per_wg, r1 = min(n, r0 + rows_per_wg);
-  for (int r = r0 + wave; r < r1; r += kWaves) {
-    const T* row = w + size_t(r) * kdim;
+
+  auto consume = [&](int item, const u32x4 (&c)[CPL]) {
+    if (item >= nitems) return;
+    const int c0 = (item % nseg) * kSeg;
+    const int last = nch - 1;
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.f;
-    for (int j0 = lane; j0 < nch; j0 += kWave * kUnroll) {
-      u32x4 c[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        if (j0 + u * kWave < nch) c[u] = load_chunk_nt<T, VEC>(row, j0 + u * kWave, kdim);
+    for (int j = 0; j < CPL; ++j) {
+      // chunks past the row were loaded as zero; pair them with a clamped
+      // (finite) x position instead of branching
+      const int q = min(c0 + lane + kWave * j, last);
+      float f[EPC];
+      unpack(c[j], f, T{});
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int j = j0 + u * kWave;
-        if (j < nch) {
-          float f[EPC];
-          unpack(c[u], f, T{});
+      for (int b = 0; b < NB; ++b) {
+        const float4* pv = reinterpret_cast<const float4*>(xs + b * kp + q * EPC);
 #pragma unroll
-          for (int b = 0; b < NB; ++b)
-#pragma unroll
-            for (int e = 0; e < EPC; ++e) acc[b] = fmaf(f[e], xs[b * kp + j * EPC + e], acc[b]);
+        for (int h = 0; h < EPC / 4; ++h) {
+          const float4 v = pv[h];
+          acc[b] = fmaf(f[4 * h], v.x, acc[b]);
+          acc[b] = fmaf(f[4 * h + 1], v.y, acc[b]);
+          acc[b] = fmaf(f[4 * h + 2], v.z, acc[b]);
+          acc[b] = fmaf(f[4 * h + 3], v.w, acc[b]);
         }
       }
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float s = wave_sum(acc[b]);
-      if (lane == 0) {
-        const size_t o = size_t(b) * n + r;
-        if (sum) {
-          const T yv = from_f<T>(s);
-          y[o] = yv;
-          sum[o] = from_f<T>(to_f(residual[o]) + to_f(yv));
-        } else {
-          y[o] = from_f<T>(residual ? s + to_f(residual[o]) : s);
-        }
+      const float t = wave_sum_u(acc[b]);
+      if (lane == 0) part[item * NB + b] = t;
+    }
+  };
+  for (int it = wave; it < nitems; it += 2 * kWaves) {
+    consume(it, ca);
+    if (it + 2 * kWaves < nitems) issue(it + 2 * kWaves, ca);
+    pin_loads();
+    if (it + kWaves >= nitems) break;
+    consume(it + kWaves, cb);
+    if (it + 3 * kWaves < nitems) issue(it + 3 * kWaves, cb);
+    pin_loads();
+  }
+  __syncthreads();
+  for (int t = tid; t < nr * NB; t += kThreads) {
+    const int rl = t / NB, b = t % NB;
+    float s = 0.f;
+    for (int g = 0; g < nseg; ++g) s += part[(rl * nseg + g) * NB + b];
+    const size_t o = size_t(b) * n + r0 + rl;
+    if (sum) {
+      const T yv = from_f<T>(s);
+      y[o] = yv;
+      sum[o] = from_f<T>(to_f(residual[o]) + to_f(yv));
+    } else {
+      y[o] = from_f<T>(residual ? s + to_f(residual[o]) : s);
+    }
+  }
+}
+
+// Element-wise variant for rows that are not whole 16-byte chunks (or
+// unaligned weights): one wave per row, any length.
+template <typename T, int NB>
+__global__ __launch_bounds__(kThreads) void gemv_scalar_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                               const T* __restrict__ residual, T* __restrict__ y,
+                                                               T* __restrict__ sum, const T* __restrict__ nw,
+                                                               float eps, int kdim, int n) {
+  extern __shared__ float xs[];
+  float* red = xs + NB * kdim;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
+  float ss[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) ss[b] = 0.f;
+  for (int i = tid; i < kdim; i += kThreads)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float v = to_f(x[size_t(b) * kdim + i]);
+      xs[b * kdim + i] = v;
+      ss[b] = fmaf(v, v, ss[b]);
+    }
+  if (nw != nullptr) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float t = wave_sum(ss[b]);
+      if (lane == 0) red[wave * NB + b] = t;
+    }
+    __syncthreads();
+    float inv[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float t = 0.f;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) t += red[v * NB + b];
+      inv[b] = 1.0f / sqrtf(t / float(kdim) + eps);
+    }
+    for (int i = tid; i < kdim; i += kThreads) {
+      const float g = to_f(nw[i]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) xs[b * kdim + i] = to_f(from_f<T>(xs[b * kdim + i] * inv[b] * g));
+    }
+  }
+  __syncthreads();
+  const int r = blockIdx.x * kWaves + wave;
+  if (r >= n) return;
+  float acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+  for (int i = lane; i < kdim; i += kWave) {
+    const float f = to_f(w[size_t(r) * kdim + i]);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = fmaf(f, xs[b * kdim + i], acc[b]);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float s = wave_sum_u(acc[b]);
+    if (lane == 0) {
+      const size_t o = size_t(b) * n + r;
+      if (sum) {
+        const T yv = from_f<T>(s);
+        y[o] = yv;
+        sum[o] = from_f<T>(to_f(residual[o]) + to_f(yv));
+      } else {
+        y[o] = from_f<T>(residual ? s + to_f(residual[o]) : s);
       }
     }
   }
+}
+
+template <typename K>
+int set_max_lds(K* kern, bool& done) {
+  if (!done) {
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    max_lds_per_block()));
+    done = true;
+  }
+  return MKQ_OK;
 }
 
 template <typename T, int NB>
 int launch(const T* x, const T* w, const T* residual, T* y, T* sum, const T* nw, float eps, int kdim, int n,
            hipStream_t stream) {
   constexpr int EPC = Epc<T>::value;
-  const size_t lds = sizeof(float) * (NB * size_t((kdim + EPC - 1) / EPC * EPC) + kWaves * NB);
+  const bool vec = (kdim % EPC == 0) && aligned16(w);
+  if (!vec) {
+    const size_t lds = sizeof(float) * (size_t(NB) * kdim + kWaves * NB);
+    if (lds > size_t(max_lds_per_block()))
+      return set_error(MKQ_ERR_UNSUPPORTED, "gemv: in_features=%d too large for LDS staging", kdim);
+    static bool attr = false;
+    const int rc = set_max_lds(&gemv_scalar_kernel<T, NB>, attr);
+    if (rc != MKQ_OK) return rc;
+    gemv_scalar_kernel<T, NB><<<(n + kWaves - 1) / kWaves, kThreads, lds, stream>>>(x, w, residual, y, sum, nw, eps,
+                                                                                    kdim, n);
+    MKQ_LAUNCH_CHECK("gemv_scalar_kernel");
+    return MKQ_OK;
+  }
+  const int nch = kdim / EPC;
+  // 8 chunks per lane (8 KB of bf16 per item) for long rows, 4 for short ones.
+  const bool wide = nch > 4 * kWave;
+  const int seg = kWave * (wide ? 8 : 4);
+  const int nseg = (nch + seg - 1) / seg;
+  // About two workgroups per CU: each keeps 8 items in flight.
+  const int ncu = cu_count();
+  const int rows_per_wg = max(1, (n + 2 * ncu - 1) / (2 * ncu));
+  const int grid = (n + rows_per_wg - 1) / rows_per_wg;
+  const size_t lds = sizeof(float) * (size_t(NB) * kdim + kWaves * NB + size_t(rows_per_wg) * nseg * NB);
   if (lds > size_t(max_lds_per_block()))
     return set_error(MKQ_ERR_UNSUPPORTED, "gemv: in_features=%d too large for LDS staging", kdim);
-  const bool vec = (kdim % EPC == 0) && aligned16(w);
-  static bool attr_set = false;
-  if (!attr_set) {
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<T, NB, true>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block()));
-    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<T, NB, false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, max_lds_per_block()));
-    attr_set = true;
+  if (wide) {
+    static bool attr = false;
+    const int rc = set_max_lds(&gemv_kernel<T, NB, 8>, attr);
+    if (rc != MKQ_OK) return rc;
+    gemv_kernel<T, NB, 8><<<grid, kThreads, lds, stream>>>(x, w, residual, y, sum, nw, eps, kdim, n, rows_per_wg);
+  } else {
+    static bool attr = false;
+    const int rc = set_max_lds(&gemv_kernel<T, NB, 4>, attr);
+    if (rc != MKQ_OK) return rc;
+    gemv_kernel<T, NB, 4><<<grid, kThreads, lds, stream>>>(x, w, residual, y, sum, nw, eps, kdim, n, rows_per_wg);
   }
-  const int rows = 2 * kWaves;
-  const int grid = (n + rows - 1) / rows;
-  if (vec)
-    gemv_kernel<T, NB, true><<<grid, kThreads, lds, stream>>>(x, w, residual, y, sum, nw, eps, kdim, n, rows);
-  else
-    gemv_kernel<T, NB, false><<<grid, kThreads, lds, stream>>>(x, w, residual, y, sum, nw, eps, kdim, n, rows);
   MKQ_LAUNCH_CHECK("gemv_kernel");
   return MKQ_OK;
 }
