@@ -402,11 +402,26 @@ def bench_layer(mk, inputs, timer, steps, warmup, batches):
         graph.replay()
         torch.cuda.synchronize()
         cold["graph_median_us"] = timer.pipelined(graph.replay, steps, cold=True)
+        cold["graph_warm_median_us"] = timer.pipelined(graph.replay, steps, cold=False)
+        # A graph replay costs a fixed launch (~4-5 us here) that one 3-kernel
+        # layer does not amortize; a serving loop captures a whole decode
+        # step.  Eight layer steps in one graph, per layer (warm: the eight
+        # reuse one layer's weights, so only the first would be cold).
+        n_graph = 8
+        graph_n = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph_n, stream=s):
+            for _ in range(n_graph):
+                fn()
+        graph_n.replay()
+        torch.cuda.synchronize()
+        cold["graph8_warm_per_layer_us"] = timer.pipelined(graph_n.replay, steps, cold=False) / n_graph
         out[f"layer_linear_moe_b{b}"] = cold
         log(f"decode_layer (gated delta + out_proj + MoE) b={b}: {cold['median_us']:.2f} us cold in stream "
             f"({cold['gbps']:.0f} GB/s), {cold['warm_median_us']:.2f} us warm, "
-            f"{cold['isolated_event_median_us']:.2f} us isolated launch, {cold['graph_median_us']:.2f} us graph replay")
-        del x, w, lin, graph
+            f"{cold['isolated_event_median_us']:.2f} us isolated launch, {cold['graph_median_us']:.2f} us graph replay, "
+            f"{cold['graph_warm_median_us']:.2f} us warm graph replay, "
+            f"{cold['graph8_warm_per_layer_us']:.2f} us per layer of an 8-layer graph (warm)")
+        del x, w, lin, graph, graph_n
         torch.cuda.empty_cache()
     return out
 

@@ -3,7 +3,9 @@
 Drop-in for the decode surface of the reference package of the same name
 (reference ``mega_kernel_qwen36/__init__.py:1-89``): the decode dataclasses and
 ops, ``extension_available`` and the text-config factories.  The vision
-encoder and the MPK task-graph planner are not part of this package.
+encoder is not part of this package.  The decode task-graph planner
+(``mpk_graph``) builds the reference's plans, and ``executor`` runs them on
+the HIP kernels.
 """
 
 from .config import (
@@ -32,9 +34,33 @@ from .ops import (
     moe_decode_status,
 )
 from ._lib import library_path, load_library
+from .mpk_graph import (
+    CompiledPlan,
+    EventSpec,
+    LaunchStep,
+    TaskGraph,
+    TaskSpec,
+    TensorSpec,
+    WorkerConfig,
+    build_batch_specialized_plans,
+    build_qwen36_decode_tgraph,
+)
+from .executor import DecodeLayerWeights, DecodePlanExecutor, DecodeStepResult
 
 __all__ = [
+    "CompiledPlan",
     "DecodeLayerResult",
+    "DecodeLayerWeights",
+    "DecodePlanExecutor",
+    "DecodeStepResult",
+    "EventSpec",
+    "LaunchStep",
+    "TaskGraph",
+    "TaskSpec",
+    "TensorSpec",
+    "WorkerConfig",
+    "build_batch_specialized_plans",
+    "build_qwen36_decode_tgraph",
     "DenseFfnWeights",
     "FullAttentionInputs",
     "GatedMoeWeights",
