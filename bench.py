@@ -442,6 +442,18 @@ def pmc_workload(mk, inputs, name, launches=10):
     elif name == "dense":
         x, w = inputs.make_dense(batch=1)
         fn = lambda: mk.dense_ffn_decode(x, w)  # noqa: E731
+    elif name == "dense_b8":  # the MFMA path
+        x, w = inputs.make_dense(batch=8)
+        fn = lambda: mk.dense_ffn_decode(x, w)  # noqa: E731
+    elif name == "layer":  # decode_layer: gated delta rule + out_proj (the projection GEMV) + MoE
+        import dataclasses
+
+        x, w, k = inputs.make_moe(batch=1)
+        lin = inputs.make_gated_delta(batch=1)
+        proj = (torch.randn(2048, 32 * 128, generator=torch.Generator().manual_seed(999)) * 0.02).to(
+            "cuda", torch.bfloat16)
+        lin = dataclasses.replace(lin, out_proj=proj)
+        fn = lambda: mk.decode_layer(0, x, w, linear_attention=lin, top_k=k)  # noqa: E731
     elif name == "attn":
         inp = inputs.make_attention(seq_len=32768)
         fn = lambda: mk.full_attention_decode(inp)  # noqa: E731
@@ -563,7 +575,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--ops", default="moe,dense,attn,linear,layer")
-    ap.add_argument("--pmc-workload", choices=("moe", "dense", "attn", "linear", "copy"), default=None,
+    ap.add_argument("--pmc-workload", choices=("moe", "dense", "dense_b8", "attn", "linear", "layer", "copy"),
+                    default=None,
                     help="run one op (or a 256 MiB copy) 10 times after flushes for a rocprofv3 --pmc pass; no JSON")
     ap.add_argument("--quick", action="store_true", help="batch 1 / 32K only")
     ap.add_argument("--cpu-budget", type=float, default=25.0,

@@ -56,17 +56,43 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x,
   issue(wave + kWaves, cb);
   pin_loads();
 
-  // x -> LDS (FP32), with its sum of squares for the optional norm.
+  // x -> LDS (FP32) with 16-byte loads, all of a thread's issued at once,
+  // and its sum of squares for the optional norm.
+  constexpr int kStage = 8;  // chunks per thread per pass (a pass covers kStage * 256 chunks)
+  const int xch = nch;       // chunks per batch row
+  const rsrc_t xr = make_rsrc(x, uint32_t(NB) * uint32_t(kdim) * uint32_t(sizeof(T)));
   float ss[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) ss[b] = 0.f;
-  for (int i = tid; i < kp; i += kThreads)
+  for (int f0 = tid; f0 < NB * xch; f0 += kStage * kThreads) {
+    u32x4 v[kStage];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const float v = i < kdim ? to_f(x[size_t(b) * kdim + i]) : 0.f;
-      xs[b * kp + i] = v;
-      ss[b] = fmaf(v, v, ss[b]);
+    for (int r = 0; r < kStage; ++r) {
+      const int f = f0 + r * kThreads;
+      v[r] = buf_load16(xr, f < NB * xch ? uint32_t(f) * 16u : 0xFFFFFFF0u);
     }
+#pragma unroll
+    for (int r = 0; r < kStage; ++r) {
+      const int f = f0 + r * kThreads;
+      if (f < NB * xch) {
+        const int b = f / xch, c = f % xch;
+        float e[EPC];
+        unpack(v[r], e, T{});
+        float sq = 0.f;
+        float4* dst = reinterpret_cast<float4*>(xs + b * kp + c * EPC);
+#pragma unroll
+        for (int h = 0; h < EPC / 4; ++h) {
+          dst[h] = make_float4(e[4 * h], e[4 * h + 1], e[4 * h + 2], e[4 * h + 3]);
+          sq = fmaf(e[4 * h], e[4 * h], sq);
+          sq = fmaf(e[4 * h + 1], e[4 * h + 1], sq);
+          sq = fmaf(e[4 * h + 2], e[4 * h + 2], sq);
+          sq = fmaf(e[4 * h + 3], e[4 * h + 3], sq);
+        }
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) ss[bb] += bb == b ? sq : 0.f;
+      }
+    }
+  }
   if (nw != nullptr) {
     // Every workgroup normalises the whole of x itself (a few KB): no
     // hand-off between workgroups.
@@ -84,10 +110,27 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const T* __restrict__ x,
       for (int v = 0; v < kWaves; ++v) t += red[v * NB + b];
       inv[b] = 1.0f / sqrtf(t / float(kdim) + eps);
     }
-    for (int i = tid; i < kdim; i += kThreads) {
-      const float g = to_f(nw[i]);
+    const rsrc_t nr = make_rsrc(nw, uint32_t(kdim) * uint32_t(sizeof(T)));
+    for (int c0 = tid; c0 < xch; c0 += kStage * kThreads) {
+      u32x4 g[kStage];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) xs[b * kp + i] = to_f(from_f<T>(xs[b * kp + i] * inv[b] * g));
+      for (int r = 0; r < kStage; ++r) g[r] = buf_load16(nr, c0 + r * kThreads < xch ? uint32_t(c0 + r * kThreads) * 16u
+                                                                                       : 0xFFFFFFF0u);
+#pragma unroll
+      for (int r = 0; r < kStage; ++r) {
+        const int c = c0 + r * kThreads;
+        if (c < xch) {
+          float gf[EPC];
+          unpack(g[r], gf, T{});
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+              float* px = xs + b * kp + c * EPC + e;
+              *px = to_f(from_f<T>(*px * inv[b] * gf[e]));
+            }
+        }
+      }
     }
   }
   __syncthreads();
@@ -232,7 +275,7 @@ template <typename T, int NB>
 int launch(const T* x, const T* w, const T* residual, T* y, T* sum, const T* nw, float eps, int kdim, int n,
            hipStream_t stream) {
   constexpr int EPC = Epc<T>::value;
-  const bool vec = (kdim % EPC == 0) && aligned16(w);
+  const bool vec = (kdim % EPC == 0) && aligned16(w) && aligned16(x) && (nw == nullptr || aligned16(nw));
   if (!vec) {
     const size_t lds = sizeof(float) * (size_t(NB) * kdim + kWaves * NB);
     if (lds > size_t(max_lds_per_block()))
