@@ -286,19 +286,22 @@ int mkq_gated_rms_norm(int dtype, const void* x, const void* gate, const void* w
                        int rows, int dim, float eps, void* stream);
 
 /* One Qwen3.6 linear-attention step around and through the recurrence, in
- * three launches on `stream` with no host work between them:
- *   mixed = silu(conv(x_mixed))   (mkq_causal_conv1d_update, conv_state in place)
+ * one launch on `stream`:
+ *   mixed = silu(conv(x_mixed))   (as mkq_causal_conv1d_update, conv_state in place)
  *   q, k, v = the [k_heads*key_dim | k_heads*key_dim | v_heads*value_dim]
- *             parts of mixed, read in place
+ *             parts of mixed
  *   o = gated delta rule with q/k L2 norm and q_scale (state updated in place)
- *   out = mkq_gated_rms_norm(o, z, norm_weight, eps)
+ *   out = gated RMSNorm of o (as mkq_gated_rms_norm(o, z, norm_weight, eps))
+ * bit-identical to those three calls in sequence.
  * x_mixed [batch, C] with C = 2*k_heads*key_dim + v_heads*value_dim;
- * conv_state [batch, C, conv_state_len]; conv_weight [C, conv_state_len+1];
- * conv_bias [C] or NULL; state [batch, v_heads, key_dim, value_dim] FP32;
- * g, beta [batch, v_heads] FP32; z, out [batch, v_heads, value_dim];
- * norm_weight [value_dim].  The workspace (mixed and o) is sized by
- * mkq_linear_attention_step_workspace_bytes and 256-byte aligned; it holds
- * no state between calls.  No counterpart in the reference. */
+ * conv_state [batch, C, conv_state_len], conv_state_len <= 7;
+ * conv_weight [C, conv_state_len+1]; conv_bias [C] or NULL;
+ * state [batch, v_heads, key_dim, value_dim] FP32; g, beta [batch, v_heads]
+ * FP32; z, out [batch, v_heads, value_dim]; norm_weight [value_dim].  The
+ * workspace (the recurrence output handed to the row norms and arrival
+ * counts) is sized by mkq_linear_attention_step_workspace_bytes, 256-byte
+ * aligned and zero-filled once before its first use: each call leaves its
+ * counts at zero.  No counterpart in the reference. */
 size_t mkq_linear_attention_step_workspace_bytes(int dtype, int batch, int k_heads, int v_heads,
                                                  int key_dim, int value_dim);
 int mkq_linear_attention_step(int dtype, const void* x_mixed, void* conv_state, const void* conv_weight,

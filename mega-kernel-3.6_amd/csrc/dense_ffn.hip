@@ -634,31 +634,6 @@ __device__ __forceinline__ f32x4 fold_hi_lo(f32x4 a) {
   return r;
 }
 
-// Partials cross workgroups (and XCDs) through agent-coherent accesses: the
-// stores write through to memory and the loads bypass the XCD-private L2
-// copies, so no cache writeback or invalidation (an agent-scope fence) is
-// needed.
-__device__ __forceinline__ void store_partial(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_partial(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Per-pair arrival: each thread waits until its partial stores are complete
-// (acknowledged by memory), the barrier gathers the workgroup, then one
-// thread counts the arrival; the workgroup learns whether it came last.  A
-// workgroup that reads the final count reads the partials only after it, so
-// it sees every split's complete stores.
-__device__ __forceinline__ bool arrive_last(unsigned* cnt, unsigned splits, int* flag) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0)
-    *flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1u ? 1 : 0;
-  __syncthreads();
-  return *flag != 0;
-}
-
 // Writes the 32x8 hi/lo-folded results of the workgroup's 4 waves (two tiles
 // each) to LDS: red[wave][row][col].
 __device__ __forceinline__ void stash_pair(const f32x4 (&acc)[2], float (*red)[kPairRows][kMfmaRows], int wave,

@@ -15,6 +15,7 @@
 // with the mean and rsqrt in FP32, the roundings of the model's module.
 //
 // Both are a few KB per step: latency-bound single launches.
+#include "linear_common.h"
 #include "mkq_host.h"
 
 using namespace mkq;
@@ -22,7 +23,6 @@ using namespace mkq;
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxTaps = 8;
 
 // grid: (ceil(C / 256), B); one thread per (b, c).
 template <typename T>
@@ -38,18 +38,16 @@ __global__ __launch_bounds__(kThreads) void conv1d_update_kernel(const T* __rest
   const T* wc = w + size_t(c) * (s_len + 1);
   // Fully unrolled over the maximum width so the window stays in registers.
   const float xv = to_f(x[row]);
-  float win[kMaxTaps];
+  float win[kMaxConvTaps], wv[kMaxConvTaps];
 #pragma unroll
-  for (int t = 0; t < kMaxTaps; ++t) win[t] = t < s_len ? to_f(st[t]) : (t == s_len ? xv : 0.f);
-  float acc = bias ? to_f(bias[c]) : 0.f;
+  for (int t = 0; t < kMaxConvTaps; ++t) {
+    win[t] = t < s_len ? to_f(st[t]) : (t == s_len ? xv : 0.f);
+    wv[t] = t <= s_len ? to_f(wc[t]) : 0.f;
+  }
+  const float y = conv_channel<T, kMaxConvTaps>(win, wv, bias ? to_f(bias[c]) : 0.f, s_len, silu_act != 0);
 #pragma unroll
-  for (int t = 0; t < kMaxTaps; ++t)
-    if (t <= s_len) acc = fmaf(to_f(wc[t]), win[t], acc);
-#pragma unroll
-  for (int t = 0; t + 1 < kMaxTaps; ++t)
+  for (int t = 0; t + 1 < kMaxConvTaps; ++t)
     if (t < s_len) st[t] = from_f<T>(win[t + 1]);
-  float y = to_f(from_f<T>(acc));
-  if (silu_act) y = to_f(from_f<T>(silu(y)));
   out[row] = from_f<T>(y);
 }
 
@@ -62,19 +60,7 @@ __global__ __launch_bounds__(kThreads) void gated_rms_norm_kernel(const T* __res
   const int r = blockIdx.x * (kThreads / kWave) + wave_id();
   if (r >= rows) return;  // wave-uniform
   const T* xr = x + size_t(r) * d;
-  float ss = 0.f;
-  for (int i = lane; i < d; i += kWave) {
-    const float v = to_f(xr[i]);
-    ss = fmaf(v, v, ss);
-  }
-  const float inv = 1.0f / sqrtf(wave_sum(ss) / float(d) + eps);
-  const T* zr = z + size_t(r) * d;
-  T* orow = out + size_t(r) * d;
-  for (int i = lane; i < d; i += kWave) {
-    const float n = to_f(from_f<T>(to_f(xr[i]) * inv));
-    const float t = to_f(from_f<T>(to_f(w[i]) * n));
-    orow[i] = from_f<T>(t * silu(to_f(zr[i])));
-  }
+  gated_norm_row<T>([&](int i) { return to_f(xr[i]); }, z + size_t(r) * d, w, out + size_t(r) * d, d, eps, lane);
 }
 
 template <typename T>
@@ -106,7 +92,7 @@ extern "C" int mkq_causal_conv1d_update(int dtype, const void* x, void* conv_sta
                                         int silu_activation, void* stream) {
   clear_error();
   MKQ_REQUIRE(batch > 0 && channels > 0 && state_len > 0, "causal_conv1d_update: sizes must be positive");
-  MKQ_REQUIRE(state_len < kMaxTaps, "causal_conv1d_update: state_len %d > %d", state_len, kMaxTaps - 1);
+  MKQ_REQUIRE(state_len < kMaxConvTaps, "causal_conv1d_update: state_len %d > %d", state_len, kMaxConvTaps - 1);
   MKQ_REQUIRE(batch <= 65535, "causal_conv1d_update: batch too large");
   MKQ_REQUIRE(x && conv_state && weight && out, "causal_conv1d_update: null tensor pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);

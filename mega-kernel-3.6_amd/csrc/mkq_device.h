@@ -176,6 +176,31 @@ __device__ __forceinline__ void buf_storef(rsrc_t r, uint32_t off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)off, 0, 0);
 }
 
+// Partials cross workgroups (and XCDs) through agent-coherent accesses: the
+// stores write through to memory and the loads bypass the XCD-private L2
+// copies, so no cache writeback or invalidation (an agent-scope fence) is
+// needed.
+__device__ __forceinline__ void store_partial(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_partial(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Per-pair arrival: each thread waits until its partial stores are complete
+// (acknowledged by memory), the barrier gathers the workgroup, then one
+// thread counts the arrival; the workgroup learns whether it came last.  A
+// workgroup that reads the final count reads the partials only after it, so
+// it sees every split's complete stores.
+__device__ __forceinline__ bool arrive_last(unsigned* cnt, unsigned splits, int* flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1u ? 1 : 0;
+  __syncthreads();
+  return *flag != 0;
+}
+
 // Streaming (read-once) variant for weights: non-temporal hint.
 template <typename T, bool VEC>
 __device__ __forceinline__ u32x4 load_chunk_nt(const T* __restrict__ row, int j, int n) {

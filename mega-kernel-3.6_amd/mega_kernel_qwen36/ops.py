@@ -556,12 +556,13 @@ def linear_attention_step(
     eps: float = 1e-6,
 ) -> torch.Tensor:
     """One Qwen3.6 linear-attention decode step from the projected q/k/v row
-    to the gated-norm output, in three launches with no host work between
-    them: causal conv update of x_mixed [batch, 2*k_heads*Dk + Hv*Dv]
-    (conv_state updated in place), the gated delta rule with q/k L2 norm
-    reading q, k and v from the conv output in place (state [batch, Hv, Dk,
-    Dv] FP32 updated in place), and the gated RMS norm with z [batch, Hv, Dv].
-    Returns out [batch, Hv, Dv].  No counterpart in the reference."""
+    to the gated-norm output, in one launch: causal conv update of x_mixed
+    [batch, 2*k_heads*Dk + Hv*Dv] (conv_state updated in place), the gated
+    delta rule with q/k L2 norm on the conv output (state [batch, Hv, Dk, Dv]
+    FP32 updated in place), and the gated RMS norm with z [batch, Hv, Dv].
+    Bit-identical to causal_conv1d_update, linear_attention_decode and
+    gated_rms_norm called in sequence.  Returns out [batch, Hv, Dv].  No
+    counterpart in the reference."""
     _require_extension("linear_attention_step", x_mixed, conv_state, conv_weight, state, g, beta, z, norm_weight)
     for name, t in (("conv_state", conv_state), ("state", state)):
         if not t.is_contiguous():

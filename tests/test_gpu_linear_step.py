@@ -154,3 +154,43 @@ def test_linear_attention_step_equals_composition(batch, hk, hv, dk, dv, dtype):
     # to f16 between the ops), to the FP32 state tolerance.
     _, ref_st = oracle.gated_delta_decode(np32(q), np32(k), np32(v), np_st, np32(gg), np32(beta), qk_l2norm=True)
     np.testing.assert_allclose(st.cpu().numpy(), ref_st, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("batch,hk,hv,dk,dv,state_len,bias,dtype", [
+    (2, 16, 32, 128, 128, 3, False, torch.bfloat16),  # Qwen3.6 heads, two rows
+    (2, 2, 6, 64, 96, 3, True, torch.bfloat16),       # a ragged last column slice, rep 3
+    (1, 1, 2, 200, 40, 5, True, torch.float16),       # width 6 (the 8-tap variant), key_dim > 128
+])
+def test_linear_attention_step_two_steps_equal_composition(batch, hk, hv, dk, dv, state_len, bias, dtype):
+    """Two steps in a row through the one launch (conv state rewritten by the
+    last workgroup reading each q/k head, the arrival counts left at zero by
+    the first call) are bit-identical to two rounds of the separate ops."""
+    c = 2 * hk * dk + hv * dv
+    g = torch.Generator().manual_seed(900 + dk)
+
+    def r(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to("cuda", dtype)
+
+    cs = r(batch, c, state_len)
+    cw = r(c, state_len + 1, scale=0.5)
+    cb = r(c, scale=0.1) if bias else None
+    st = (torch.randn(batch, hv, dk, dv, generator=g) * 0.1).cuda()
+    nw = r(dv, scale=0.2) + 1.0
+    cs2, st2 = cs.clone(), st.clone()
+    for step in range(2):
+        x = r(batch, c)
+        z = r(batch, hv, dv)
+        gg = -torch.nn.functional.softplus(torch.randn(batch, hv, generator=g)).cuda()
+        beta = torch.sigmoid(torch.randn(batch, hv, generator=g)).cuda()
+        out = mk.linear_attention_step(x, cs, cw, st, gg, beta, z, nw, k_heads=hk, conv_bias=cb)
+        mixed = mk.causal_conv1d_update(x, cs2, cw, bias=cb)
+        q = mixed[:, :hk * dk].reshape(batch, hk, dk)
+        k = mixed[:, hk * dk:2 * hk * dk].reshape(batch, hk, dk)
+        v = mixed[:, 2 * hk * dk:].reshape(batch, hv, dv)
+        o, st2 = mk.linear_attention_decode(mk.LinearAttentionInputs(q=q, k=k, v=v, state=st2, g=gg, beta=beta,
+                                                                     qk_l2norm=True))
+        want = mk.gated_rms_norm(o, z, nw)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"step {step}"
+        assert torch.equal(cs, cs2), f"step {step}"
+        assert torch.equal(st, st2), f"step {step}"

@@ -300,8 +300,8 @@ def test_linear_step_entry_validates_on_the_host_without_gpu():
     any launch."""
     lib = _lib.load_library()
     need = lib.mkq_linear_attention_step_workspace_bytes(_lib.MKQ_DTYPE_BF16, 2, 16, 32, 128, 128)
-    c = 2 * 16 * 128 + 32 * 128
-    assert need == ((2 * c * 2 + 255) // 256 + (2 * 32 * 128 * 2 + 255) // 256) * 256
+    # two fixed arrays of 16384 arrival counts, then FP32 output rows [2, 32, 128]
+    assert need == 2 * 16384 * 4 + 2 * 32 * 128 * 4
     assert lib.mkq_linear_attention_step_workspace_bytes(99, 2, 16, 32, 128, 128) == 0
     raw = ctypes.create_string_buffer(need + 512)
     ws = (ctypes.addressof(raw) + 255) // 256 * 256
@@ -315,6 +315,14 @@ def test_linear_step_entry_validates_on_the_host_without_gpu():
     bad = list(args)
     bad[14] = 512  # key_dim
     assert call(_lib.MKQ_DTYPE_BF16, *bad, ws, need, None) == _lib.MKQ_ERR_UNSUPPORTED
+    bad = list(args)
+    bad[11] = 600  # batch * v_heads above the 16384 arrival counts
+    assert call(_lib.MKQ_DTYPE_BF16, *bad, ws, need, None) == _lib.MKQ_ERR_UNSUPPORTED
+    assert b"v_heads" in lib.mkq_last_error()
+    bad = list(args)
+    bad[4] = 8  # conv_state_len: width 9 > 8 taps
+    assert call(_lib.MKQ_DTYPE_BF16, *bad, ws, need, None) == _lib.MKQ_ERR_INVALID
+    assert b"conv_state_len" in lib.mkq_last_error()
 
 
 def test_paged_append_entry_rejects_missing_rows_without_gpu():
