@@ -663,8 +663,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     }
     if (tid == 0) {
       misc[16] = 0;
-      misc[18] = 0;  // one-row routing progress (slots handed out)
+      misc[18] = 0;  // one-row routing: K + 1 once the route weights are in LDS
     }
+    if (MB == 1 && tid < K) sel_e[tid] = 0;  // one-row routing: slot tid's expert + 1, 0 until decided
     __syncthreads();
     MOE_MARK(1);
     if (tid < B) {
@@ -758,18 +759,23 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     // round is then one wave-wide max of the lane heads and a ballot for the
     // lowest lane holding it -- the lowest expert index among equal logits,
     // the reference's tie rule -- after which that lane pops its head.
-    // After round s wave 0 writes slot s's expert to LDS and advances a
-    // counter there; each wave issues its first group of gate/up rows as soon
-    // as the counter covers the group's slots, while the later rounds run.
-    // The counter reaches K + 1 once the route weights (softmax over the K
-    // selected logits) are in LDS too.
+    // After round s wave 0 writes slot s's expert + 1 into the slot's LDS
+    // word (one store, no ordering wait inside the round); each wave issues
+    // its first group of gate/up rows as soon as the words of the group's
+    // slots are set, while the later rounds run.  A counter reaches K + 1
+    // once the route weights (softmax over the K selected logits) are in LDS
+    // too.
     int* const ready = misc + 18;
     // The round after which every slot of this wave's first group is known.
+    // Wave 0 runs the rounds, so it takes the groups of the last wave (the
+    // last slot at the batch-1 shape) and issues no loads inside the rounds:
+    // issuing there waited on the CU's memory queue (~0.3 us) and delayed
+    // every later round.
     const int nw_total = nwg * kWaves;
-    const int gw = wave * nwg + wg;
+    const int gw = ((wave + kWaves - 1) % kWaves) * nwg + wg;
     const int ntask = K * I;
     const int first_ready = min(K - 1, min(gw * kGU + kGU - 1, ntask - 1) / I);
-    auto slot_expert = [&](int u) { return __builtin_amdgcn_readfirstlane(sel_e[u]); };
+    auto slot_expert = [&](int u) { return __builtin_amdgcn_readfirstlane(sel_e[u]) - 1; };
     auto slot_weight = [&](int u) { return sel_w[u]; };
     const size_t hrow = size_t(min(h0 + wave, H - 1));
 
@@ -808,6 +814,14 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         __builtin_amdgcn_s_sleep(1);
       }
     };
+    // Waits (bounded) until slots 0..n are decided.  Wave 0 writes the slot
+    // words in order, and one wave's LDS stores land in issue order.
+    auto wait_slot = [&](int n) {
+      for (unsigned polls = 0; polls < kSpinLimit; ++polls) {
+        if (__hip_atomic_load(sel_e + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    };
     u32x4 gA[kGU][HC], uA[kGU][HC], gB[kGU][HC], uB[kGU][HC];
     if (wave == 0) {
       int my_e;
@@ -815,12 +829,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       const bool routed =
           route_row<EL>(make_rsrc(w.logits + (wg % kCopies) * logit_copy_words(E), uint32_t(E) * 8u), E, K, tag,
                         lane, my_e, my_w, [&](int s, int e) {
-                          if (lane == s) sel_e[s] = e;
-                          if (lane == 0) __hip_atomic_store(ready, s + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                          if (s == first_ready) {
-                            issue_gu(gw, gA, uA);
-                            pin_loads();
-                          }
+                          if (lane == s)  // lane s holds slot s's expert
+                            __hip_atomic_store(sel_e + s, e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                         });
       if (!routed && lane == 0) misc[16] = 1;
       if (lane < K) sel_w[lane] = my_w;
@@ -829,15 +839,20 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
         a.idx[lane] = my_e;
         a.wts[lane] = my_w;
       }
+      // Wave 0's own rows only now: by this time the other waves' rows fill
+      // the CU's memory queue, and an issue that waits for queue space must
+      // not hold back the route weights every wave needs.
+      issue_gu(gw, gA, uA);
+      pin_loads();
       if (s0 < Is) issue_shared_gu();
       issue_shared_down();
       pin_loads();
     } else {
-      wait_ready(first_ready);
+      wait_slot(first_ready);
       issue_gu(gw, gA, uA);
       pin_loads();
     }
-    wait_ready(K);  // route weights in LDS
+    wait_ready(K);  // route weights in LDS (and every slot word)
     MOE_MARK(3);
     // Shared-expert act of the waves that own a shared row (its rows arrived
     // long ago), before their routed rows: phase 3 needs both.  This code
