@@ -223,14 +223,17 @@ __global__ __launch_bounds__(kThreads) void ffn_gateup_kernel(const T* __restric
   }
 }
 
-// K2: grid.x = ceil(H / rows_per_wg); block = 256.
+// K2: grid.x = ceil(H / rows_per_wg); block = NT (256, or 512 when two
+// workgroups' act copies would not fit one CU's LDS: then one workgroup of 8
+// waves per CU shares one copy, with as many loads in flight as two of 4).
 // LDS: NB*ip floats (act) + rows_per_wg*kQuarters*NB floats (quarter sums).
-template <typename T, int NB, bool VEC, int CPL>
-__global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restrict__ act, const T* __restrict__ wd,
+template <typename T, int NB, bool VEC, int CPL, int NT>
+__global__ __launch_bounds__(NT) void ffn_down_kernel(const float* __restrict__ act, const T* __restrict__ wd,
                                                             const T* __restrict__ x, T* __restrict__ out, int h,
                                                             int inter, int add_residual, int rows_per_wg,
                                                             int act_ld) {
   constexpr int EPC = Epc<T>::value;
+  constexpr int NW = NT / kWave;
   extern __shared__ float smem[];
   const int ip = round_up(inter, EPC);
   const int nch = ip / EPC;                          // chunks per row
@@ -262,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
   };
   // Weight loads of the first two items go out before act is staged.
   issue(wave, ca);
-  issue(wave + kWaves, cb);
+  issue(wave + NW, cb);
   pin_loads();
 
   // act -> LDS: 16-byte buffer loads, kActUnroll per thread in flight (act
@@ -274,22 +277,22 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
     // One descriptor over all NB rows (a per-row descriptor would depend on the
     // lane's row and force a readfirstlane loop around every load).
     const rsrc_t ar = make_rsrc(act, uint32_t(NB - 1) * uint32_t(act_ld) * 4u + uint32_t(inter) * 4u);
-    for (int f0 = tid; f0 < NB * q4; f0 += kActUnroll * kThreads) {
+    for (int f0 = tid; f0 < NB * q4; f0 += kActUnroll * NT) {
       u32x4 v[kActUnroll];
 #pragma unroll
       for (int r = 0; r < kActUnroll; ++r) {
-        const int f = f0 + r * kThreads;
+        const int f = f0 + r * NT;
         const int b = f / q4, c4 = f % q4;
         v[r] = buf_load16(ar, f < NB * q4 ? (uint32_t(b) * uint32_t(act_ld) + uint32_t(c4) * 4u) * 4u : 0xFFFFFFF0u);
       }
 #pragma unroll
       for (int r = 0; r < kActUnroll; ++r) {
-        const int f = f0 + r * kThreads;
+        const int f = f0 + r * NT;
         if (f < NB * q4) *reinterpret_cast<u32x4*>(a + size_t(f) * 4) = v[r];
       }
     }
   } else {
-    for (int k = tid; k < ip; k += kThreads) {
+    for (int k = tid; k < ip; k += NT) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) a[b * ip + k] = k < inter ? act[size_t(b) * act_ld + k] : 0.f;
     }
@@ -307,16 +310,16 @@ __global__ __launch_bounds__(kThreads) void ffn_down_kernel(const float* __restr
       if (lane == 0) part[item * NB + b] = s;
     }
   };
-  for (int item = wave; item < nitems; item += 2 * kWaves) {
+  for (int item = wave; item < nitems; item += 2 * NW) {
     finish(item, ca);
-    issue(item + 2 * kWaves, ca);
+    issue(item + 2 * NW, ca);
     pin_loads();
-    finish(item + kWaves, cb);
-    issue(item + 3 * kWaves, cb);
+    finish(item + NW, cb);
+    issue(item + 3 * NW, cb);
     pin_loads();
   }
   __syncthreads();
-  for (int t = tid; t < nr * NB; t += kThreads) {
+  for (int t = tid; t < nr * NB; t += NT) {
     const int i = t / NB, b = t % NB;
     float s = 0.f;
 #pragma unroll
@@ -802,10 +805,14 @@ int launch_nb(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, T*
   const int max_lds = max_lds_per_block();
   const int hp = round_up(h, EPC), ip = round_up(inter, EPC);
 
-  // Both kernels: two workgroups per CU, rows split evenly.
+  // Both kernels: two workgroups per CU, rows split evenly -- except a down
+  // kernel whose act copy (NB rows, FP32) fills more than half of the LDS:
+  // one workgroup of 8 waves per CU.
   const int rows1 = (inter + 2 * ncu - 1) / (2 * ncu);
   const int grid1 = (inter + rows1 - 1) / rows1;
-  const int rows2 = (h + 2 * ncu - 1) / (2 * ncu);
+  const bool wide2 = 2 * sizeof(float) * (size_t(NB) * ip + size_t(h + 2 * ncu - 1) / (2 * ncu) * kQuarters * NB) >
+                     size_t(max_lds);
+  const int rows2 = wide2 ? (h + ncu - 1) / ncu : (h + 2 * ncu - 1) / (2 * ncu);
   const int grid2 = (h + rows2 - 1) / rows2;
 
   const size_t lds1 = sizeof(float) * (size_t(NB) * hp + kWaves * NB + size_t(2) * rows1 * NB);
@@ -816,14 +823,19 @@ int launch_nb(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, T*
   static bool attr_set = false;
   if (!attr_set) {
     if (int rc = set_lds_limit(&ffn_gateup_kernel<T, NB, VEC, CPL1>)) return rc;
-    if (int rc = set_lds_limit(&ffn_down_kernel<T, NB, VEC, CPL2>)) return rc;
+    if (int rc = set_lds_limit(&ffn_down_kernel<T, NB, VEC, CPL2, kThreads>)) return rc;
+    if (int rc = set_lds_limit(&ffn_down_kernel<T, NB, VEC, CPL2, 2 * kThreads>)) return rc;
     attr_set = true;
   }
   ffn_gateup_kernel<T, NB, VEC, CPL1><<<grid1, kThreads, lds1, stream>>>(x, nw, wg, wu, act, h, inter, eps, inter,
                                                                         rows1);
   MKQ_LAUNCH_CHECK("ffn_gateup_kernel");
-  ffn_down_kernel<T, NB, VEC, CPL2><<<grid2, kThreads, lds2, stream>>>(act, wd, x, out, h, inter, add_residual, rows2,
-                                                                      inter);
+  if (wide2)
+    ffn_down_kernel<T, NB, VEC, CPL2, 2 * kThreads><<<grid2, 2 * kThreads, lds2, stream>>>(
+        act, wd, x, out, h, inter, add_residual, rows2, inter);
+  else
+    ffn_down_kernel<T, NB, VEC, CPL2, kThreads><<<grid2, kThreads, lds2, stream>>>(act, wd, x, out, h, inter,
+                                                                                   add_residual, rows2, inter);
   MKQ_LAUNCH_CHECK("ffn_down_kernel");
   return MKQ_OK;
 }
