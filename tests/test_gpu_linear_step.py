@@ -160,6 +160,7 @@ def test_linear_attention_step_equals_composition(batch, hk, hv, dk, dv, dtype):
     (2, 16, 32, 128, 128, 3, False, torch.bfloat16),  # Qwen3.6 heads, two rows
     (2, 2, 6, 64, 96, 3, True, torch.bfloat16),       # a ragged last column slice, rep 3
     (1, 1, 2, 200, 40, 5, True, torch.float16),       # width 6 (the 8-tap variant), key_dim > 128
+    (2, 1, 3, 64, 320, 3, False, torch.bfloat16),     # value_dim > 256: the row norm reads z and the weight itself
 ])
 def test_linear_attention_step_two_steps_equal_composition(batch, hk, hv, dk, dv, state_len, bias, dtype):
     """Two steps in a row through the one launch (conv state rewritten by the
