@@ -226,6 +226,20 @@ int mkq_full_attention_decode_paged_rope(int dtype, const void* q, const void* k
                                          const float* cos_sin, int rotary_dim, void* workspace,
                                          size_t workspace_bytes, void* stream);
 
+/* Paged KV with both the KV append and the in-kernel RoPE: the new token is
+ * written into its block as by mkq_full_attention_decode_paged_append (the
+ * key unrotated, as the caches hold keys) and q and the keys are rotated as
+ * by mkq_full_attention_decode_paged_rope; bit-identical to
+ * mkq_full_attention_decode_append with cos_sin over the gathered contiguous
+ * cache.  Limits as for the entry points it combines.  No counterpart in the
+ * reference. */
+int mkq_full_attention_decode_paged_append_rope(int dtype, const void* q, const void* k_new, const void* v_new,
+                                                void* k_blocks, void* v_blocks, const int* block_table,
+                                                void* out, int batch, int q_heads, int kv_heads, int head_dim,
+                                                int seq_len, int block_size, int max_blocks, int num_blocks,
+                                                float scale, const float* cos_sin, int rotary_dim,
+                                                void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Recurrent linear-attention decode, reference rule.  Replaces
  *   _C.linear_attention_decode    (csrc/bindings.cpp:35, csrc/linear_attention_decode.cu:46-93)

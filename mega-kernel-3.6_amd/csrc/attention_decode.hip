@@ -747,6 +747,8 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
                                     hipFuncAttributeMaxDynamicSharedMemorySize, pagedb));
     MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, false, true>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, paged_roped));
+    MKQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<T, DT, true, true, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, paged_roped));
     attr_set = true;
   }
   MKQ_REQUIRE(size_t(ch.nch) * units < (size_t(1) << 31), "full_attention_decode: grid too large");
@@ -754,7 +756,8 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   float* part_m = part_o + size_t(batch) * hq * ch.nch * d;
   float* part_l = part_m + size_t(batch) * hq * ch.nch;
   const bool app = ap.k_new != nullptr;
-  auto* kern = paged  ? (app ? attn_chunk_kernel<T, DT, false, true, true>
+  auto* kern = paged  ? (app ? (rot > 0 ? attn_chunk_kernel<T, DT, true, true, true>
+                                       : attn_chunk_kernel<T, DT, false, true, true>)
                              : rot > 0 ? attn_chunk_kernel<T, DT, true, false, true>
                                        : attn_chunk_kernel<T, DT, false, false, true>)
                : rot > 0 ? (app ? attn_chunk_kernel<T, DT, true, true, false> : attn_chunk_kernel<T, DT, true, false, false>)
@@ -851,9 +854,6 @@ int attention_entry(const char* fn, int dtype, const void* q, const void* k_cach
       return set_error(MKQ_ERR_UNSUPPORTED,
                        "%s: the in-kernel append needs bf16/f16, head_dim %% 8 == 0 and 16-byte aligned tensors", fn);
   }
-  if (pg.table && ap.k_new && rot > 0)
-    return set_error(MKQ_ERR_UNSUPPORTED, "%s: paged KV with both the append and RoPE in one launch is not supported",
-                     fn);
   if (rot > 0) {
     MKQ_REQUIRE(rope_cs, "%s: null cos/sin pointer", fn);
     if (!fast_ok || (dtype != MKQ_DTYPE_BF16 && dtype != MKQ_DTYPE_F16) || rot < 16 || rot > head_dim ||
@@ -983,4 +983,33 @@ extern "C" int mkq_full_attention_decode_paged_append(int dtype, const void* q, 
   ap.cap = seq_len;  // unused by the paged store
   return attention_entry(fn, dtype, q, k_blocks, v_blocks, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
                          nullptr, 0, ap, pg, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mkq_full_attention_decode_paged_append_rope(int dtype, const void* q, const void* k_new,
+                                                           const void* v_new, void* k_blocks, void* v_blocks,
+                                                           const int* block_table, void* out, int batch, int q_heads,
+                                                           int kv_heads, int head_dim, int seq_len, int block_size,
+                                                           int max_blocks, int num_blocks, float scale,
+                                                           const float* cos_sin, int rotary_dim, void* workspace,
+                                                           size_t workspace_bytes, void* stream) {
+  const char* fn = "full_attention_decode_paged_append_rope";
+  if (!block_table || !k_new || !v_new || !cos_sin) {
+    clear_error();
+    return set_error(MKQ_ERR_INVALID, "%s: null tensor pointer", fn);
+  }
+  if (rotary_dim <= 0) {
+    clear_error();
+    return set_error(MKQ_ERR_INVALID, "%s: rotary_dim %d must be positive", fn, rotary_dim);
+  }
+  Paged pg;
+  pg.table = block_table;
+  pg.block_size = block_size;
+  pg.max_blocks = max_blocks;
+  pg.num_blocks = num_blocks;
+  Append ap;
+  ap.k_new = k_new;
+  ap.v_new = v_new;
+  ap.cap = seq_len;  // unused by the paged store
+  return attention_entry(fn, dtype, q, k_blocks, v_blocks, out, batch, q_heads, kv_heads, head_dim, seq_len, scale,
+                         cos_sin, rotary_dim, ap, pg, workspace, workspace_bytes, stream);
 }

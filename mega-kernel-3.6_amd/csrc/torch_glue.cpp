@@ -333,19 +333,13 @@ torch::Tensor full_attention_decode_paged(torch::Tensor q, torch::Tensor k_block
   auto ws = workspace_for(Ws::kAttention, q,
                           mkq_full_attention_decode_workspace_bytes(batch, query_heads, kv_heads, head_dim, seq));
   TORCH_CHECK(k_new.has_value() == v_new.has_value(), "k_new and v_new must be given together");
-  TORCH_CHECK(!(k_new.has_value() && cos_sin.has_value()), "the paged append does not take cos_sin");
   int rc;
   if (cos_sin.has_value()) {
     TORCH_CHECK(cos_sin->is_cuda() && cos_sin->is_contiguous() && cos_sin->scalar_type() == torch::kFloat32,
                 "cos_sin must be a contiguous float32 device tensor");
     TORCH_CHECK(cos_sin->numel() == 2 * rotary_dim, "cos_sin must hold 2 * rotary_dim values");
-    rc = mkq_full_attention_decode_paged_rope(
-        to_mkq_dtype(q), q.data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(), block_table.data_ptr<int>(),
-        out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq, static_cast<int>(k_blocks.size(1)),
-        static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)), static_cast<float>(scale),
-        cos_sin->data_ptr<float>(), static_cast<int>(rotary_dim), ws.data_ptr(), static_cast<size_t>(ws.numel()),
-        current_stream());
-  } else if (k_new.has_value()) {
+  }
+  if (k_new.has_value()) {
     MK_CHECK_INPUT((*k_new));
     MK_CHECK_INPUT((*v_new));
     TORCH_CHECK(k_new->dim() == 3 && k_new->size(0) == batch && k_new->size(1) == kv_heads &&
@@ -353,6 +347,22 @@ torch::Tensor full_attention_decode_paged(torch::Tensor q, torch::Tensor k_block
                 "k_new and v_new must be [batch, kv_heads, head_dim]");
     TORCH_CHECK(k_new->scalar_type() == q.scalar_type() && v_new->scalar_type() == q.scalar_type(),
                 "k_new/v_new dtype mismatch");
+  }
+  if (cos_sin.has_value() && k_new.has_value()) {
+    rc = mkq_full_attention_decode_paged_append_rope(
+        to_mkq_dtype(q), q.data_ptr(), k_new->data_ptr(), v_new->data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(),
+        block_table.data_ptr<int>(), out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq,
+        static_cast<int>(k_blocks.size(1)), static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)),
+        static_cast<float>(scale), cos_sin->data_ptr<float>(), static_cast<int>(rotary_dim), ws.data_ptr(),
+        static_cast<size_t>(ws.numel()), current_stream());
+  } else if (cos_sin.has_value()) {
+    rc = mkq_full_attention_decode_paged_rope(
+        to_mkq_dtype(q), q.data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(), block_table.data_ptr<int>(),
+        out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq, static_cast<int>(k_blocks.size(1)),
+        static_cast<int>(block_table.size(1)), static_cast<int>(k_blocks.size(0)), static_cast<float>(scale),
+        cos_sin->data_ptr<float>(), static_cast<int>(rotary_dim), ws.data_ptr(), static_cast<size_t>(ws.numel()),
+        current_stream());
+  } else if (k_new.has_value()) {
     rc = mkq_full_attention_decode_paged_append(
         to_mkq_dtype(q), q.data_ptr(), k_new->data_ptr(), v_new->data_ptr(), k_blocks.data_ptr(), v_blocks.data_ptr(),
         block_table.data_ptr<int>(), out.data_ptr(), batch, query_heads, kv_heads, head_dim, seq,

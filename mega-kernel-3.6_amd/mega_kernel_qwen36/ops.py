@@ -417,8 +417,8 @@ def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
     k_new/v_new the new token is token seq_len - 1 (or cache_seqlen): the
     kernel writes it into its block and uses it directly; the fallback
     writes the row first.  With cos/sin, q and the keys are rotated in the
-    kernel where it can (no append); otherwise the rows are gathered and the
-    contiguous path rotates them."""
+    kernel where it can (with or without the append); otherwise the rows are
+    gathered and the contiguous path rotates them."""
     if (inputs.k_new is None) != (inputs.v_new is None):
         raise ValueError("k_new and v_new must be given together")
     kb, vb, table = inputs.k_cache, inputs.v_cache, inputs.block_table
@@ -446,7 +446,12 @@ def _attention_paged(inputs: FullAttentionInputs) -> torch.Tensor:
     rope = inputs.cos is not None and inputs.sin is not None
     cs = _rope_in_kernel(inputs) if rope else None
     if (kb.dtype in (torch.bfloat16, torch.float16) and d % 8 == 0 and bs % 16 == 0 and q.dtype == kb.dtype
-            and not (rope and (append or cs is None))):
+            and not (rope and cs is None)):
+        if rope and append:
+            return _C.full_attention_decode_paged(q.contiguous(), kb, vb, table.to(torch.int32).contiguous(), seq,
+                                                  float(scale), k_new.to(kb.dtype).contiguous(),
+                                                  v_new.to(kb.dtype).contiguous(), cos_sin=cs,
+                                                  rotary_dim=int(inputs.rotary_dim))
         if rope:
             return _C.full_attention_decode_paged(q.contiguous(), kb.contiguous(), vb.contiguous(),
                                                   table.to(torch.int32).contiguous(), seq, float(scale),

@@ -452,3 +452,34 @@ def test_attention_paged_rope_equals_contiguous_rope(b, hq, hkv, d, t, bs, rot, 
                                                           scale=inp.scale, block_table=table, seq_len=t))
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t,bs,rot,dtype", [
+    (1, 24, 4, 256, 32768, 16, 64, torch.bfloat16),   # config 4 with RoPE and the append, 16-token blocks
+    (3, 8, 2, 128, 3001, 64, 32, torch.float16),      # ragged last block
+    (2, 40, 2, 128, 1, 16, 128, torch.bfloat16),      # the first token of a fresh block; group 20; full rotation
+])
+def test_attention_paged_append_rope_equals_write_then_attend(b, hq, hkv, d, t, bs, rot, dtype):
+    """Paged KV with both the append and RoPE in one launch: the output and
+    both pools are bit-identical to writing the unrotated new row into its
+    block with torch and then running the paged RoPE kernel; no other row
+    changes."""
+    inp = make_attention(batch=b, q_heads=hq, kv_heads=hkv, head_dim=d, seq_len=t, seed=650 + t, dtype=dtype)
+    pk, pv, table, _, _ = _paged_case(inp, bs, 651 + t)
+    g = torch.Generator().manual_seed(652 + t)
+    k_new = torch.randn(b, hkv, d, generator=g).to("cuda", dtype)
+    v_new = torch.randn(b, hkv, d, generator=g).to("cuda", dtype)
+    ang = torch.rand(rot, generator=g) * 6.0
+    cos, sin = torch.cos(ang)[None], torch.sin(ang)[None]
+    pk2, pv2 = pk.clone(), pv.clone()
+    blk = table[:, (t - 1) // bs].long()
+    pk2[blk, (t - 1) % bs] = k_new
+    pv2[blk, (t - 1) % bs] = v_new
+    want = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk2, pv2, cos=cos, sin=sin, rotary_dim=rot,
+                                                           scale=inp.scale, block_table=table, seq_len=t))
+    got = mk.full_attention_decode(mk.FullAttentionInputs(inp.q, pk, pv, cos=cos, sin=sin, rotary_dim=rot,
+                                                          scale=inp.scale, block_table=table, seq_len=t,
+                                                          k_new=k_new, v_new=v_new))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(pk, pk2) and torch.equal(pv, pv2)

@@ -340,6 +340,28 @@ def test_paged_append_entry_rejects_missing_rows_without_gpu():
                 None) == _lib.MKQ_ERR_UNSUPPORTED
 
 
+def test_paged_append_rope_entry_validates_on_the_host_without_gpu():
+    """mkq_full_attention_decode_paged_append_rope rejects missing tensors and
+    a non-positive rotary_dim before any launch."""
+    lib = _lib.load_library()
+    b, hq, hkv, d, t = 1, 4, 2, 64, 40
+    nbytes = lib.mkq_full_attention_decode_workspace_bytes(b, hq, hkv, d, t)
+    raw = ctypes.create_string_buffer(nbytes + 512)
+    ws = (ctypes.addressof(raw) + 255) // 256 * 256
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    call = lib.mkq_full_attention_decode_paged_append_rope
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, None, 16, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert call(_lib.MKQ_DTYPE_BF16, p, None, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, p, 16, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, p, p, b, hq, hkv, d, t, 16, 3, 8, 1.0, p, 0, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID
+    assert b"rotary_dim" in lib.mkq_last_error()
+    assert call(_lib.MKQ_DTYPE_BF16, p, p, p, p, p, p, p, b, hq, hkv, d, t, 24, 3, 8, 1.0, p, 16, ws, nbytes,
+                None) == _lib.MKQ_ERR_INVALID  # block_size not a multiple of 16
+
+
 def test_paged_rope_entry_validates_on_the_host_without_gpu():
     """mkq_full_attention_decode_paged_rope checks its arguments before any
     launch: a null table or cos/sin and a non-positive rotary_dim or a block
