@@ -307,6 +307,19 @@ def bench_attention(mk, inputs, timer, steps, warmup, seq_lens):
                 out[f"attn_paged{bs}_t32768"] = r
                 log(f"attention T={t} paged ({bs}-token blocks): {r['median_us']:.2f} us cold in stream, "
                     f"{r['warm_median_us']:.2f} us warm")
+                # The decode step's whole attention in one launch: the new
+                # token's row written into its block (the same values it
+                # already holds, so every step sees the same cache) and q and
+                # the keys rotated inside the kernel.
+                pa = mk.FullAttentionInputs(q=inp.q, k_cache=pk, v_cache=pv,
+                                            block_table=perm.to(torch.int32)[None].cuda(), seq_len=t,
+                                            k_new=inp.k_cache[:, t - 1].clone(), v_new=inp.v_cache[:, t - 1].clone(),
+                                            cos=rope.cos, sin=rope.sin, rotary_dim=64)
+                r = measure(timer, lambda: mk.full_attention_decode(pa), steps, warmup,  # noqa: B023
+                            attn_bytes(1, 24, 4, 256, t))
+                out[f"attn_paged{bs}_append_rope_t32768"] = r
+                log(f"attention T={t} paged ({bs}-token blocks) with KV append and RoPE: {r['median_us']:.2f} us "
+                    f"cold in stream, {r['warm_median_us']:.2f} us warm")
                 del pk, pv
         del inp
         torch.cuda.empty_cache()

@@ -78,10 +78,10 @@ struct Mfma<f16_t> {
 // 8 floats -> one 16-byte chunk of T (round to nearest even).
 __device__ __forceinline__ u32x4 pack8(const float (&f)[8], bf16_t) {
   u32x4 r;
-  r.x = uint32_t(f2bf_bits(f[0])) | (uint32_t(f2bf_bits(f[1])) << 16);
-  r.y = uint32_t(f2bf_bits(f[2])) | (uint32_t(f2bf_bits(f[3])) << 16);
-  r.z = uint32_t(f2bf_bits(f[4])) | (uint32_t(f2bf_bits(f[5])) << 16);
-  r.w = uint32_t(f2bf_bits(f[6])) | (uint32_t(f2bf_bits(f[7])) << 16);
+  r.x = f2bf2_bits(f[0], f[1]);
+  r.y = f2bf2_bits(f[2], f[3]);
+  r.z = f2bf2_bits(f[4], f[5]);
+  r.w = f2bf2_bits(f[6], f[7]);
   return r;
 }
 __device__ __forceinline__ u32x4 pack8(const float (&f)[8], f16_t) {
@@ -97,17 +97,15 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8], f16_t) {
 }
 
 // Rotate-half RoPE of one 16-byte chunk: x' = x cos + p sin', p = the partner
-// chunk, cos / sin' = 8 values each in LDS (sin' already negated for the
-// lower half).  Two rounded products, a rounded sum, then the rounding to T,
+// chunk, cos / sin' = 8 values each (c0 c1 / s0 s1; sin' already negated for
+// the lower half).  Two rounded products, a rounded sum, then the rounding to T,
 // as reference.py:91-114's torch ops do: no contraction into an FMA and no
 // fused f32->f16 mixed FMA (the register barriers keep each value FP32).
 template <typename T>
-__device__ __forceinline__ u32x4 rope8(u32x4 xq, u32x4 pq, const float* cs, const float* sn) {
+__device__ __forceinline__ u32x4 rope8(u32x4 xq, u32x4 pq, f32x4 c0, f32x4 c1, f32x4 s0, f32x4 s1) {
   float xf[8], pf[8], of[8];
   unpack(xq, xf, T{});
   unpack(pq, pf, T{});
-  const f32x4 c0 = reinterpret_cast<const f32x4*>(cs)[0], c1 = reinterpret_cast<const f32x4*>(cs)[1];
-  const f32x4 s0 = reinterpret_cast<const f32x4*>(sn)[0], s1 = reinterpret_cast<const f32x4*>(sn)[1];
   const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
   const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
 #pragma unroll
@@ -287,6 +285,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   // ROPE: cos and the signed sin (rotate_half negates the upper half) of the
   // rotary dims, in LDS after the staging/merge area.
   const int rhc = ROPE ? rot / 16 : 0;  // partner chunk distance
+  // ROPE: rot/8 rotary chunks per row (a power of two, 2^rlg); this lane's
+  // chunk of the row in the key rotation.
+  const int rlg = ROPE ? __builtin_ctz(unsigned(rot / 8)) : 0;
+  const int rc = lane & ((1 << rlg) - 1);
   float* rope_l = reinterpret_cast<float*>(smem + rope_lds_off);
   static_assert(2 * kMaxD <= 2 * kThreads, "two cos/sin values per thread fill the table");
   unsigned char* stage = smem + size_t(wave) * stage_bytes(DT);
@@ -325,8 +327,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int d0 = 32 * s + 8 * grp;
-      if (d0 < rot) qop[s] = __builtin_bit_cast(V8, rope8<T>(__builtin_bit_cast(u32x4, qop[s]), qpart[s],
-                                                             rope_l + d0, rope_l + rot + d0));
+      if (d0 < rot) {
+        const f32x4* cp = reinterpret_cast<const f32x4*>(rope_l + d0);
+        const f32x4* sp = reinterpret_cast<const f32x4*>(rope_l + rot + d0);
+        qop[s] = __builtin_bit_cast(V8, rope8<T>(__builtin_bit_cast(u32x4, qop[s]), qpart[s], cp[0], cp[1], sp[0],
+                                                 sp[1]));
+      }
     }
   }
 
@@ -342,6 +348,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
       const int qi = lane + kWave * i;
       *reinterpret_cast<u32x4*>(stage + (qi / CPR) * KSTR + (qi % CPR) * 16) = kreg[i];
     }
+    // The next pass's K into the freed registers before the staged tile is
+    // patched (APP) and rotated (ROPE), so that work overlaps the loads.
+    uint32_t nob;
+    if (pf) {
+      const rsrc_t nk = tile_src(kc, kr, t0 + kWgTokens, nob);
+#pragma unroll
+      for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(nk, nob + voff[i]);
+      pin_loads();
+    }
     // APP: the new token's key over its stale row (same wave, program order).
     const int ar = arow - t0;
     const bool arow_here = owner && ar >= 0 && ar < kTT;
@@ -350,25 +365,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
     }
     if constexpr (ROPE) {
       // Rotary chunks, k' = k cos + rotate_half(k) sin: the tile's 16 * rot/8
-      // of them spread over the wave's lanes (chunk j = row j / nrc, chunk
-      // j % nrc).  A chunk and its partner (j ^ rhc) fall in the same group of
-      // 64, so both lanes read before either writes, and groups are whole
-      // rows.
-      const int nrc = rot / 8;
-      for (int j = lane; j < kTT * nrc; j += kWave) {
-        unsigned char* rowp = stage + (j / nrc) * KSTR;
-        const int c = j % nrc;
-        const u32x4 own = *reinterpret_cast<const u32x4*>(rowp + c * 16);
-        const u32x4 pq = *reinterpret_cast<const u32x4*>(rowp + (c ^ rhc) * 16);
-        *reinterpret_cast<u32x4*>(rowp + c * 16) = rope8<T>(own, pq, rope_l + c * 8, rope_l + rot + c * 8);
+      // of them spread over the wave's lanes, two per pass (chunks j and
+      // j + 64; chunk j is row j >> rlg, chunk rc of the row, the same for
+      // both since rot/8 divides 64).  A chunk and its partner (rc ^ rhc) fall
+      // in the same group of 64 and groups are whole rows; each pass reads
+      // its four chunks before it writes.  Past the last chunk the second of
+      // the pair repeats the first, which writes the same value twice.
+      const f32x4 c0 = reinterpret_cast<const f32x4*>(rope_l + rc * 8)[0];
+      const f32x4 c1 = reinterpret_cast<const f32x4*>(rope_l + rc * 8)[1];
+      const f32x4 s0 = reinterpret_cast<const f32x4*>(rope_l + rot + rc * 8)[0];
+      const f32x4 s1 = reinterpret_cast<const f32x4*>(rope_l + rot + rc * 8)[1];
+      const int nchk = kTT << rlg;
+      for (int j = lane; j < nchk; j += kWave) {
+        unsigned char* r0 = stage + (j >> rlg) * KSTR;
+        const u32x4 own0 = *reinterpret_cast<const u32x4*>(r0 + rc * 16);
+        const u32x4 pq0 = *reinterpret_cast<const u32x4*>(r0 + (rc ^ rhc) * 16);
+        *reinterpret_cast<u32x4*>(r0 + rc * 16) = rope8<T>(own0, pq0, c0, c1, s0, s1);
       }
-    }
-    uint32_t nob;
-    if (pf) {
-      const rsrc_t nk = tile_src(kc, kr, t0 + kWgTokens, nob);
-#pragma unroll
-      for (int i = 0; i < VCH; ++i) kreg[i] = buf_load16<kAuxStream>(nk, nob + voff[i]);
-      pin_loads();
     }
     f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll

@@ -49,12 +49,16 @@ __device__ __forceinline__ float to_f(bf16_t v) { return __uint_as_float(uint32_
 __device__ __forceinline__ float to_f(f16_t v) { return float(v); }
 __device__ __forceinline__ float to_f(float v) { return v; }
 
-// float -> bfloat16, round to nearest even; NaN stays NaN.
-__device__ __forceinline__ uint16_t f2bf_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+// float -> bfloat16, round to nearest even; NaN stays NaN.  Bit for bit the
+// rule u' = (u + 0x7fff + ((u >> 16) & 1)) >> 16 for non-NaN u and
+// (u >> 16) | 0x40 for NaN, which the compiler's float -> __bf16 conversion
+// (gfx950's v_cvt_pk_bf16_f32) computes (checked against that rule on all
+// 2^32 inputs, denormals and NaNs included).  The conversion is left to the
+// compiler, which tracks the instruction's register hazards.
+__device__ __forceinline__ uint16_t f2bf_bits(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+// Two of them packed: lo in bits 0..15, hi in bits 16..31.
+__device__ __forceinline__ uint32_t f2bf2_bits(float lo, float hi) {
+  return uint32_t(f2bf_bits(lo)) | (uint32_t(f2bf_bits(hi)) << 16);
 }
 
 template <typename T>
