@@ -318,10 +318,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_chunk_kernel(
   // same rounding as the keys); q's loads were issued before K/V, so this
   // waits for them alone.
   if constexpr (ROPE) {
+    // Every entry of the 2 * kMaxD-float table is written (zeros past 2 * rot):
+    // with the store under a condition, the compiler moved the cos/sin loads
+    // into that branch, behind the K/V loads, and waited for all of them.
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int t = threadIdx.x + j * kThreads;
-      if (t < 2 * rot) rope_l[t] = t >= rot && t < rot + rot / 2 ? -cs_ld[j] : cs_ld[j];
+      rope_l[t] = t >= rot && t < rot + rot / 2 ? -cs_ld[j] : cs_ld[j];
     }
     __syncthreads();
 #pragma unroll
@@ -779,7 +782,7 @@ int launch_fast(const void* q, const void* k, const void* v, void* out, int batc
   // The cos/sin table (ROPE) and then the block ids (PG) follow the
   // staging/merge area.
   const size_t rope_off = (lds + 15) / 16 * 16;
-  const size_t blk_off = rope_off + (rot > 0 ? size_t(2 * rot) * sizeof(float) : 0);
+  const size_t blk_off = rope_off + (rot > 0 ? size_t(2 * kMaxD) * sizeof(float) : 0);
   const int nblk = paged ? (ch.chunk_tokens + pg.block_size - 1) / pg.block_size + 2 : 0;
   const size_t lds_all = paged ? blk_off + size_t(nblk) * sizeof(int) : rot > 0 ? blk_off : lds;
   kern<<<dim3(ch.nch * units), kThreads, lds_all, stream>>>(
