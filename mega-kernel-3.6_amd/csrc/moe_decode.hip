@@ -420,9 +420,11 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // and generation can no longer be trusted, so every launch writes NaN and
   // leaves without publishing anything until the host clears the workspace
   // (mkq_moe_decode_status with reset).  Taken through LDS after the first
-  // barrier, so the whole workgroup takes the same branch.
+  // barrier, so the whole workgroup takes the same branch.  Thread 0 stores
+  // it into LDS only after the norm: a store under `tid == 0` here made the
+  // compiler wait for every load issued so far (x, the norm weight, w_sg)
+  // before wave 0 issued its router row.
   const unsigned err_at_start = __hip_atomic_load(w.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (tid == 0) misc[17] = int(err_at_start);
   // One-row path: the residual of this wave's output row, fetched now; after
   // the expert weights have streamed through, x is no longer in the L2.
   float x_res = 0.f;
@@ -460,7 +462,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     for (int e = tid; e < E; e += kThreads) emask[e] = 0u;
     // Wave b: RMSNorm of batch row b into LDS and its shared-gate dot; no
     // other wave reads the row before the routing barrier.
-    if (tid == 0) misc[16] = 0;
+    if (tid == 0) {
+      misc[16] = 0;
+      misc[17] = int(err_at_start);
+    }
     if (wave < B) {
       float* xr_l = xn + wave * Hp;
       float ss = 0.f;
@@ -663,6 +668,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     }
     if (tid == 0) {
       misc[16] = 0;
+      misc[17] = int(err_at_start);
       misc[18] = 0;  // one-row routing: K + 1 once the route weights are in LDS
     }
     if (MB == 1 && tid < K) sel_e[tid] = 0;  // one-row routing: slot tid's expert + 1, 0 until decided
