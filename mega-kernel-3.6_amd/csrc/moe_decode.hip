@@ -691,6 +691,33 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   }
   const unsigned tag = gen + 1u;
   if (tid == 0) put_tagged(w.presence + wg, 0.f, tag);
+  // WG 0 advances the generation once every WG of this launch has read it
+  // (its presence word carries the tag).  Nothing of this launch reads the
+  // generation word after its start, so this may run as soon as every WG is
+  // known to have started: the one-row instance runs it in wave 1 of WG 0,
+  // which reaches the end of its gate/up rows ~1 us before the workgroup's
+  // last wave, so the check's round trip is off the kernel's tail.
+  auto advance_gen = [&]() {
+    const rsrc_t pr = make_rsrc(w.presence, uint32_t(nwg) * 8u);
+    bool seen = false;
+    for (unsigned polls = 0; polls < kSpinLimit && !seen; ++polls) {
+      bool ready = true;
+      for (int q = lane; q < (nwg + 1) / 2; q += kWave) {
+        const u32x4 v = buf_load16<kAuxCoherent>(pr, uint32_t(q) * 16u);
+        ready = ready & (v.y == tag) & (2 * q + 1 >= nwg || v.w == tag);
+      }
+      seen = __all(ready);
+      if (!seen) __builtin_amdgcn_s_sleep(1);
+    }
+    // After a timed-out wait the generation is left alone: the error word
+    // keeps every later launch out of the tagged arrays until a reset.
+    if (lane == 0) {
+      if (!seen)
+        __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        __hip_atomic_store(w.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
   // This XCD's copies of the published act and shared act.  The multi-row
   // path publishes B times as many act words and keeps one copy: there the
   // extra stores cost more than the shorter wait saves.
@@ -875,6 +902,7 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       compute_gu(grp + nw_total, gB, uB);
     }
     MOE_MARK(4);
+    if (wg == 0 && wave == 1) advance_gen();
     // Down rows of (this wave's output row, expert of slot s): needed only
     // after the act exchange, so they are issued once the whole WG's gate/up
     // rows are consumed and stream during the exchange.  A CU serves its
@@ -1328,27 +1356,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       }
   }
   }  // multi-row path
-  // WG 0 advances the generation once every WG of this launch has read it.
-  if (wg == 0 && wave == 0) {
-    const rsrc_t pr = make_rsrc(w.presence, uint32_t(nwg) * 8u);
-    bool seen = false;
-    for (unsigned polls = 0; polls < kSpinLimit && !seen; ++polls) {
-      bool ready = true;
-      for (int q = lane; q < (nwg + 1) / 2; q += kWave) {
-        const u32x4 v = buf_load16<kAuxCoherent>(pr, uint32_t(q) * 16u);
-        ready = ready & (v.y == tag) & (2 * q + 1 >= nwg || v.w == tag);
-      }
-      seen = __all(ready);
-      if (!seen) __builtin_amdgcn_s_sleep(1);
-    }
-    // After a timed-out wait the generation is left alone: the error word
-    // keeps every later launch out of the tagged arrays until a reset.
-    if (lane == 0) {
-      if (!seen)
-        __hip_atomic_store(w.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      else
-        __hip_atomic_store(w.gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  if constexpr (MB > 1) {
+    if (wg == 0 && wave == 0) advance_gen();
   }
   MOE_MARK(7);
 }
