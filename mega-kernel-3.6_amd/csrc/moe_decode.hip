@@ -425,10 +425,16 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   // compiler wait for every load issued so far (x, the norm weight, w_sg)
   // before wave 0 issued its router row.
   const unsigned err_at_start = __hip_atomic_load(w.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // One-row path: the residual of this wave's output row, fetched now; after
-  // the expert weights have streamed through, x is no longer in the L2.
+  // The residual of this wave's (first) output row, fetched now: after the
+  // expert weights have streamed through, x is no longer in the L2, and a
+  // load at the end would add a cold round trip to the tail.  Several batch
+  // rows: lane b holds batch row b's value (clamped in range, so no branch).
   float x_res = 0.f;
-  if constexpr (MB == 1) x_res = to_f(a.x[min(wg * a.rows_per_wg + wave, H - 1)]);
+  if constexpr (MB == 1) {
+    x_res = to_f(a.x[min(wg * a.rows_per_wg + wave, H - 1)]);
+  } else {
+    x_res = to_f(a.x[size_t(min(lane, B - 1)) * H + min(wg * a.rows_per_wg + wave, H - 1)]);
+  }
   // Router and shared gate/up rows: one row per wave (rows wg + nwg * w) with
   // one batch row; with several batch rows, wave b takes every router and
   // shared row of the WG (rows wg + nwg * j) for batch row b.
@@ -1349,8 +1355,9 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       if (b < B) {
         float s = fmaf(sgf[b], wave_sum_u(dot_row<T, IC>(c, sact_l + b * Isp, Is, lane)), part[hl * MB + b]);
         const size_t o = size_t(b) * H + h0 + hl;
+        const float xr = __shfl(x_res, b, kWave);  // prefetched for the wave's first row
         if (lane == 0) {
-          if (a.add_residual) s += to_f(a.x[o]);
+          if (a.add_residual) s += hl == wave ? xr : to_f(a.x[o]);
           a.out[o] = from_f<T>(timed_out ? NAN : s);
         }
       }
