@@ -1350,17 +1350,56 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
     } else {
       load_row<T, VEC, IC>(a.sd + size_t(h0 + hl) * Is, Is, true, lane, c);
     }
+    if (B > kMaxB / 2) {
+      // The MB shared-expert dots of this row are summed over the wave
+      // together (from B = 5 on; below, one reduction per row costs less):
+      // a butterfly halves the values a lane holds at each of log2(MB)
+      // steps (lane bit k picks the half kept), then the lanes that hold
+      // the same value add across the remaining lane bits.  Lane L ends with
+      // the total of batch row bitrev(L mod MB).  Rows b >= B read row
+      // B - 1's shared act and are not written.
+      constexpr int LGB = MB == 2 ? 1 : MB == 4 ? 2 : 3;
+      static_assert(MB == 2 || MB == 4 || MB == 8, "power-of-two batch rows");
+      float dv[MB];
 #pragma unroll
-    for (int b = 0; b < MB; ++b)
-      if (b < B) {
-        float s = fmaf(sgf[b], wave_sum_u(dot_row<T, IC>(c, sact_l + b * Isp, Is, lane)), part[hl * MB + b]);
-        const size_t o = size_t(b) * H + h0 + hl;
-        const float xr = __shfl(x_res, b, kWave);  // prefetched for the wave's first row
-        if (lane == 0) {
-          if (a.add_residual) s += hl == wave ? xr : to_f(a.x[o]);
-          a.out[o] = from_f<T>(timed_out ? NAN : s);
+      for (int b = 0; b < MB; ++b) dv[b] = dot_row<T, IC>(c, sact_l + min(b, B - 1) * Isp, Is, lane);
+#pragma unroll
+      for (int k = 0; k < LGB; ++k) {
+        const int half = MB >> (k + 1);
+        const bool hi = (lane >> k) & 1;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+          const float keep = hi ? dv[i + half] : dv[i];
+          const float send = hi ? dv[i] : dv[i + half];
+          dv[i] = keep + __shfl_xor(send, 1 << k, kWave);
         }
       }
+      float tot = dv[0];
+#pragma unroll
+      for (int m = MB; m < kWave; m <<= 1) tot += __shfl_xor(tot, m, kWave);
+      int bb = 0;  // the batch row this lane's total belongs to
+#pragma unroll
+      for (int k = 0; k < LGB; ++k) bb |= ((lane >> k) & 1) << (LGB - 1 - k);
+      const float xr = __shfl(x_res, bb, kWave);  // lane b of x_res holds batch row b's residual
+      if (lane < MB && bb < B) {
+        const size_t o = size_t(bb) * H + h0 + hl;
+        float s = fmaf(sgf[bb], tot, part[hl * MB + bb]);
+        if (a.add_residual) s += hl == wave ? xr : to_f(a.x[o]);
+        a.out[o] = from_f<T>(timed_out ? NAN : s);
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+        if (b < B) {
+          float s = fmaf(sgf[b], wave_sum_u(dot_row<T, IC>(c, sact_l + b * Isp, Is, lane)), part[hl * MB + b]);
+          const size_t o = size_t(b) * H + h0 + hl;
+          const float xr = __shfl(x_res, b, kWave);  // prefetched for the wave's first row
+          if (lane == 0) {
+            if (a.add_residual) s += hl == wave ? xr : to_f(a.x[o]);
+            a.out[o] = from_f<T>(timed_out ? NAN : s);
+          }
+        }
+    }
   }
   }  // multi-row path
   if constexpr (MB > 1) {
