@@ -483,3 +483,43 @@ def test_attention_paged_append_rope_equals_write_then_attend(b, hq, hkv, d, t, 
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.equal(pk, pk2) and torch.equal(pv, pv2)
+
+
+def test_attention_paged_append_rope_graph_replay():
+    """Paged KV with the append and RoPE in one launch, captured in a HIP
+    graph: every replay writes the same row and returns the eager output bit
+    for bit, with an eager contiguous call sharing the workspace between
+    replays."""
+    t, bs, rot = 4096, 16, 64
+    inp = make_attention(seq_len=t, seed=671)
+    pk, pv, table, _, _ = _paged_case(inp, bs, 672)
+    g = torch.Generator().manual_seed(673)
+    k_new = torch.randn(1, 4, 256, generator=g).to("cuda", torch.bfloat16)
+    v_new = torch.randn(1, 4, 256, generator=g).to("cuda", torch.bfloat16)
+    ang = torch.rand(rot, generator=g) * 6.0
+    cos, sin = torch.cos(ang)[None], torch.sin(ang)[None]
+    args = mk.FullAttentionInputs(inp.q, pk, pv, cos=cos, sin=sin, rotary_dim=rot, scale=inp.scale,
+                                  block_table=table, seq_len=t, k_new=k_new, v_new=v_new)
+    eager = mk.full_attention_decode(args)
+    pk_e, pv_e = pk.clone(), pv.clone()
+    other = make_attention(batch=1, q_heads=8, kv_heads=2, head_dim=128, seq_len=3000, seed=674)
+    other_ref = mk.full_attention_decode(other)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mk.full_attention_decode(args)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        res = mk.full_attention_decode(args)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(res, eager)
+        assert torch.equal(pk, pk_e) and torch.equal(pv, pv_e)
+        with torch.cuda.stream(s):
+            mid = mk.full_attention_decode(other)
+        torch.cuda.synchronize()
+        assert torch.equal(mid, other_ref)

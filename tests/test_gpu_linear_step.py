@@ -195,3 +195,37 @@ def test_linear_attention_step_two_steps_equal_composition(batch, hk, hv, dk, dv
         assert torch.equal(out, want), f"step {step}"
         assert torch.equal(cs, cs2), f"step {step}"
         assert torch.equal(st, st2), f"step {step}"
+
+
+def test_linear_attention_step_graph_replay():
+    """The one-launch step captured in a HIP graph: each replay advances the
+    conv and recurrent states in place exactly as an eager step on copies
+    does (outputs and both states bit for bit), and eager steps of another
+    shape on the capture stream, which share the step's workspace and its
+    arrival counts, run between the replays."""
+    hk, hv, dk, dv = 16, 32, 128, 128
+    x, cs, cw, st, gg, beta, z, nw = _step_case(1, hk, hv, dk, dv, torch.bfloat16, 811)
+    ox, ocs, ocw, ost, ogg, obeta, oz, onw = _step_case(2, 2, 4, 64, 32, torch.bfloat16, 812)
+    cs_e, st_e = cs.clone(), st.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up on copies: the captured buffers keep their initial states
+        mk.linear_attention_step(x, cs.clone(), cw, st.clone(), gg, beta, z, nw, k_heads=hk)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out_g = mk.linear_attention_step(x, cs, cw, st, gg, beta, z, nw, k_heads=hk)
+    ocs_e, ost_e = ocs.clone(), ost.clone()
+    for step in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        out_e = mk.linear_attention_step(x, cs_e, cw, st_e, gg, beta, z, nw, k_heads=hk)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), f"replay {step}"
+        assert torch.equal(cs, cs_e) and torch.equal(st, st_e), f"replay {step}"
+        with torch.cuda.stream(s):
+            other = mk.linear_attention_step(ox, ocs, ocw, ost, ogg, obeta, oz, onw, k_heads=2)
+        other_e = mk.linear_attention_step(ox, ocs_e, ocw, ost_e, ogg, obeta, oz, onw, k_heads=2)
+        torch.cuda.synchronize()
+        assert torch.equal(other, other_e) and torch.equal(ost, ost_e), f"replay {step}"
