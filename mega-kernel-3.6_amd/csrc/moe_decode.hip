@@ -774,7 +774,10 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
       if (lane < kActCopies) put_tagged(w.sact + lane * sact_copy_words(Is) + size_t(wave) * Is + s, silu(g) * u, tag);
     }
   };
-  if constexpr (MB > 1) publish_shared();
+  // The multi-row instance publishes its shared-expert act in phase 2, after
+  // its first routed gate/up rows are issued: the loop loads a second row
+  // pair cold (Is > nwg), and waiting for it here held the routing back by
+  // ~2 us at B = 8.
 
   if constexpr (MB == 1) {
     // Shared rows (and this wave's 1 KB shared down row, used in phase 3) are
@@ -1156,6 +1159,8 @@ __global__ __launch_bounds__(kThreads, 1) void moe_decode_kernel(MoeArgs<T> a) {
   };
   u32x4 gA[kGUM][HC], uA[kGUM][HC], gB[kGUM][HC], uB[kGUM][HC];
   issue_gu(gw, gA, uA);
+  pin_loads();
+  publish_shared();
 
   // Double-buffered: the next group is in flight while this one is reduced.
   // Groups are issued unconditionally (tasks past ntask are zero-size loads),
