@@ -515,15 +515,15 @@ __global__ __launch_bounds__(kPackThreads) void ffn_pack_x_kernel(const T* __res
   *reinterpret_cast<u32x4*>(xf + (size_t(s) * kWave + lane) * 8) = v;
 }
 
-// Accumulates the products of 32 rows of W (two 16-row tiles; the descriptor
-// `wr` starts at the first row and covers only rows of the matrix, so rows
-// past it read zero) with the B fragments of k-steps [sb, se).  Load
+// Accumulates the products of 16 NT rows of W (NT 16-row tiles; the
+// descriptor `wr` starts at the first row and covers only rows of the matrix,
+// so rows past it read zero) with the B fragments of k-steps [sb, se).  Load
 // instruction i of a batch reads rows 2i (lanes 0..31) and 2i + 1 (lanes
 // 32..63), 512 contiguous bytes each; k past kdim or past se reads zero.
-template <typename T>
+template <typename T, int NT>
 __device__ __forceinline__ void pair_mfma(rsrc_t wr, rsrc_t fr, int kdim, int sb, int se, int lane,
-                                          unsigned char* __restrict__ lds, f32x4 (&acc)[2]) {
-  constexpr int NI = kPairRows / 2;  // load instructions per batch
+                                          unsigned char* __restrict__ lds, f32x4 (&acc)[NT]) {
+  constexpr int NI = 8 * NT;  // load instructions per batch
   const int half = lane >> 5, cb = (lane & 31) * 16;  // row parity, byte in the 512-byte segment
   const uint32_t rstride = uint32_t(kdim) * 2u;
   auto woff = [&](int s0, int i) -> uint32_t {
@@ -549,12 +549,13 @@ __device__ __forceinline__ void pair_mfma(rsrc_t wr, rsrc_t fr, int kdim, int sb
 #pragma unroll
     for (int j = 0; j < kStepBatch; ++j)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(rd + 16 * t * kLdsRow + 64 * j);
         acc[t] = MfmaOp<T>::mma(a, f[j], acc[t]);
       }
   };
-  acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   // The next batch is always issued (steps past se are out-of-range loads:
   // zeros, no memory traffic), so the loop body has no branch and the waits
   // before a batch's use cover only that batch.
@@ -575,10 +576,10 @@ __device__ __forceinline__ void pair_mfma(rsrc_t wr, rsrc_t fr, int kdim, int sb
 // loaded once, before the first weight batch, and the loop streams weights
 // only (each batch used to carry 8 KB of fragment loads per 16 KB of
 // weights).  The batches are unrolled, so every fragment index is a constant.
-template <typename T, int XR>
+template <typename T, int XR, int NT>
 __device__ __forceinline__ void pair_mfma_xr(rsrc_t wr, rsrc_t fr, int kdim, int sb, int se, int lane,
-                                             unsigned char* __restrict__ lds, f32x4 (&acc)[2]) {
-  constexpr int NI = kPairRows / 2;
+                                             unsigned char* __restrict__ lds, f32x4 (&acc)[NT]) {
+  constexpr int NI = 8 * NT;
   constexpr int NB = (XR + kStepBatch - 1) / kStepBatch;
   const int half = lane >> 5, cb = (lane & 31) * 16;
   const uint32_t rstride = uint32_t(kdim) * 2u;
@@ -603,7 +604,8 @@ __device__ __forceinline__ void pair_mfma_xr(rsrc_t wr, rsrc_t fr, int kdim, int
   };
   unsigned char* wst = lds + (half * kLdsRow + cb);
   const unsigned char* rd = lds + ((lane & 15) * kLdsRow + 16 * (lane >> 4));
-  acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   issue(sb, wbuf[0]);
   pin_loads();
 #pragma unroll
@@ -618,7 +620,7 @@ __device__ __forceinline__ void pair_mfma_xr(rsrc_t wr, rsrc_t fr, int kdim, int
     for (int j = 0; j < kStepBatch; ++j) {
       if (bt * kStepBatch + j >= XR) break;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(rd + 16 * t * kLdsRow + 64 * j);
         acc[t] = MfmaOp<T>::mma(a, xr[bt * kStepBatch + j], acc[t]);
       }
@@ -637,24 +639,72 @@ __device__ __forceinline__ f32x4 fold_hi_lo(f32x4 a) {
   return r;
 }
 
-// Writes the 32x8 hi/lo-folded results of the workgroup's 4 waves (two tiles
-// each) to LDS: red[wave][row][col].
-__device__ __forceinline__ void stash_pair(const f32x4 (&acc)[2], float (*red)[kPairRows][kMfmaRows], int wave,
-                                           int lane) {
+// Writes the hi/lo-folded results of the workgroup's 4 waves (NT tiles each,
+// the first at pair row row0) to LDS: red[wave][row][col].
+template <int NT>
+__device__ __forceinline__ void stash_pair(const f32x4 (&acc)[NT], float (*red)[kPairRows][kMfmaRows], int wave,
+                                           int lane, int row0) {
   const int c = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < NT; ++t) {
     const f32x4 v = fold_hi_lo(acc[t]);
     if (c < kMfmaRows) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[wave][16 * t + 4 * g + i][c] = v[i];
+      for (int i = 0; i < 4; ++i) red[wave][row0 + 16 * t + 4 * g + i][c] = v[i];
     }
   }
 }
 
-// K1: grid = pairs1 * kSplit1, block 256.  blockIdx = kSplit1 * pair + split;
-// wave w computes matrix (w >> 1: gate, up) over part 2 * split + (w & 1) of
-// 2 * kSplit1 equal parts of k.
+// Work units of the batched kernels.  Workgroups [0, nsplit * nfull) take
+// (pair, split) units with both 16-row tiles, pair-major.  The pairs from
+// nfull on, dispatched last, are cut into (pair, split, tile) units of half
+// the size, so the launch ends on a round of small units instead of a partly
+// filled round of full ones.  tile is -1 for a full unit.  Each tile's partial
+// is the same sum of the same products either way.
+__device__ __forceinline__ void unit_of(int bid, int nsplit, int nfull, int& pair, int& q, int& tile) {
+  if (bid < nsplit * nfull) {
+    pair = bid / nsplit;
+    q = bid % nsplit;
+    tile = -1;
+  } else {
+    const int t = bid - nsplit * nfull;
+    pair = nfull + t / (2 * nsplit);
+    q = (t >> 1) % nsplit;
+    tile = t & 1;
+  }
+}
+
+// One unit's product: rows [r0, r0 + 32) of the pair, or the 16 rows of one
+// tile, of a matrix with `nrows` rows of `kdim` elements.  Leaves the folded
+// results in red[wave].
+template <typename T, int XR>
+__device__ __forceinline__ void unit_mfma(const T* __restrict__ w, int nrows, int r0, int tile, rsrc_t fr, int kdim,
+                                          int sb, int se, int lane, int wave, unsigned char* __restrict__ lds,
+                                          float (*red)[kPairRows][kMfmaRows]) {
+  if (tile < 0) {
+    const rsrc_t wr = make_rsrc(w + size_t(r0) * kdim, uint32_t(min(kPairRows, nrows - r0)) * uint32_t(kdim) * 2u);
+    f32x4 acc[2];
+    if constexpr (XR > 0)
+      pair_mfma_xr<T, XR, 2>(wr, fr, kdim, sb, se, lane, lds, acc);
+    else
+      pair_mfma<T, 2>(wr, fr, kdim, sb, se, lane, lds, acc);
+    stash_pair<2>(acc, red, wave, lane, 0);
+  } else {
+    const int rt = r0 + 16 * tile;
+    const int n = max(0, min(16, nrows - rt));
+    const rsrc_t wr = make_rsrc(w + size_t(min(rt, nrows)) * kdim, uint32_t(n) * uint32_t(kdim) * 2u);
+    f32x4 acc[1];
+    if constexpr (XR > 0)
+      pair_mfma_xr<T, XR, 1>(wr, fr, kdim, sb, se, lane, lds, acc);
+    else
+      pair_mfma<T, 1>(wr, fr, kdim, sb, se, lane, lds, acc);
+    stash_pair<1>(acc, red, wave, lane, 16 * tile);
+  }
+}
+
+// K1: grid = kSplit1 * (nfull + 2 * (pairs1 - nfull)), block 256; units as in
+// unit_of.  Wave w computes matrix (w >> 1: gate, up) over part
+// 2 * split + (w & 1) of 2 * kSplit1 equal parts of k.
 template <typename T, int XR>
 __global__ __launch_bounds__(kThreads, 2) void ffn_gateup_mfma_kernel(const T* __restrict__ wg,
                                                                       const T* __restrict__ wu,
@@ -662,35 +712,30 @@ __global__ __launch_bounds__(kThreads, 2) void ffn_gateup_mfma_kernel(const T* _
                                                                       uint16_t* __restrict__ af,
                                                                       float* __restrict__ p1,
                                                                       unsigned* __restrict__ cnt1, int nb, int h,
-                                                                      int inter) {
+                                                                      int inter, int nfull) {
   __shared__ __attribute__((aligned(16))) unsigned char stage[kWaves * kWaveLds];
   __shared__ float red[kWaves][kPairRows][kMfmaRows];
   __shared__ int flag;
   const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
-  const int pair = blockIdx.x / kSplit1, q = blockIdx.x % kSplit1;
+  int pair, q, tile;
+  unit_of(blockIdx.x, kSplit1, nfull, pair, q, tile);
   const int s1 = (h + 31) / 32;
   const int part = 2 * q + (wave & 1);
   const int sb = part * s1 / (2 * kSplit1), se = (part + 1) * s1 / (2 * kSplit1);
   const int r0 = kPairRows * pair;
-  const int rows = min(kPairRows, inter - r0);
-  const T* w = (wave >> 1) ? wu : wg;
-  const rsrc_t wr = make_rsrc(w + size_t(r0) * h, uint32_t(rows) * uint32_t(h) * 2u);
   const rsrc_t fr = make_rsrc(xf, uint32_t(s1) * 1024u);
-  f32x4 acc[2];
-  if constexpr (XR > 0)
-    pair_mfma_xr<T, XR>(wr, fr, h, sb, se, lane, stage + wave * kWaveLds, acc);
-  else
-    pair_mfma<T>(wr, fr, h, sb, se, lane, stage + wave * kWaveLds, acc);
-  stash_pair(acc, red, wave, lane);
+  unit_mfma<T, XR>((wave >> 1) ? wu : wg, inter, r0, tile, fr, h, sb, se, lane, wave, stage + wave * kWaveLds, red);
   __syncthreads();
   constexpr int kPart = 2 * kPairRows * kMfmaRows;  // floats per (pair, split)
   float* pt = p1 + size_t(pair) * kSplit1 * kPart;
   {
     const int r = tid / kMfmaRows, b = tid % kMfmaRows;  // tid < 256 = 32 rows x 8 columns
-    store_partial(pt + q * kPart + tid, red[0][r][b] + red[1][r][b]);
-    store_partial(pt + q * kPart + kPairRows * kMfmaRows + tid, red[2][r][b] + red[3][r][b]);
+    if (tile < 0 || (r >> 4) == tile) {
+      store_partial(pt + q * kPart + tid, red[0][r][b] + red[1][r][b]);
+      store_partial(pt + q * kPart + kPairRows * kMfmaRows + tid, red[2][r][b] + red[3][r][b]);
+    }
   }
-  if (!arrive_last(cnt1 + pair, kSplit1, &flag)) return;
+  if (!arrive_last(cnt1 + pair, pair < nfull ? kSplit1 : 2 * kSplit1, &flag)) return;
   // Last split of this pair: act = silu(gate) * up for its 32 rows, written
   // as the down projection's B fragments (k = intermediate index); rows past
   // `inter` (up to the next multiple of 32) and columns past nb are zero.
@@ -712,42 +757,37 @@ __global__ __launch_bounds__(kThreads, 2) void ffn_gateup_mfma_kernel(const T* _
   if (tid == 0) __hip_atomic_store(cnt1 + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// K2: grid = pairs2 * kSplit2, block 256.  blockIdx = kSplit2 * pair + split;
-// wave w covers part 4 * split + w of 4 * kSplit2 equal parts of k (the
-// intermediate axis).
+// K2: grid = kSplit2 * (nfull + 2 * (pairs2 - nfull)), block 256; units as in
+// unit_of.  Wave w covers part 4 * split + w of 4 * kSplit2 equal parts of k
+// (the intermediate axis).
 template <typename T, int XR>
 __global__ __launch_bounds__(kThreads, 2) void ffn_down_mfma_kernel(const T* __restrict__ wd,
                                                                     const uint16_t* __restrict__ af,
                                                                     const T* __restrict__ x, T* __restrict__ out,
                                                                     float* __restrict__ p2,
                                                                     unsigned* __restrict__ cnt2, int nb, int h,
-                                                                    int inter, int add_residual) {
+                                                                    int inter, int add_residual, int nfull) {
   __shared__ __attribute__((aligned(16))) unsigned char stage[kWaves * kWaveLds];
   __shared__ float red[kWaves][kPairRows][kMfmaRows];
   __shared__ int flag;
   const int tid = threadIdx.x, lane = tid % kWave, wave = wave_id();
-  const int pair = blockIdx.x / kSplit2, q = blockIdx.x % kSplit2;
+  int pair, q, tile;
+  unit_of(blockIdx.x, kSplit2, nfull, pair, q, tile);
   const int s2 = (inter + 31) / 32;
   const int part = kWaves * q + wave;
   const int sb = part * s2 / (kWaves * kSplit2), se = (part + 1) * s2 / (kWaves * kSplit2);
   const int r0 = kPairRows * pair;
-  const int rows = min(kPairRows, h - r0);
-  const rsrc_t wr = make_rsrc(wd + size_t(r0) * inter, uint32_t(rows) * uint32_t(inter) * 2u);
   const rsrc_t fr = make_rsrc(af, uint32_t(s2) * 1024u);
-  f32x4 acc[2];
-  if constexpr (XR > 0)
-    pair_mfma_xr<T, XR>(wr, fr, inter, sb, se, lane, stage + wave * kWaveLds, acc);
-  else
-    pair_mfma<T>(wr, fr, inter, sb, se, lane, stage + wave * kWaveLds, acc);
-  stash_pair(acc, red, wave, lane);
+  unit_mfma<T, XR>(wd, h, r0, tile, fr, inter, sb, se, lane, wave, stage + wave * kWaveLds, red);
   __syncthreads();
   constexpr int kPart = kPairRows * kMfmaRows;
   float* pt = p2 + size_t(pair) * kSplit2 * kPart;
   {
     const int r = tid / kMfmaRows, b = tid % kMfmaRows;
-    store_partial(pt + q * kPart + tid, red[0][r][b] + red[1][r][b] + red[2][r][b] + red[3][r][b]);
+    if (tile < 0 || (r >> 4) == tile)
+      store_partial(pt + q * kPart + tid, red[0][r][b] + red[1][r][b] + red[2][r][b] + red[3][r][b]);
   }
-  if (!arrive_last(cnt2 + pair, kSplit2, &flag)) return;
+  if (!arrive_last(cnt2 + pair, pair < nfull ? kSplit2 : 2 * kSplit2, &flag)) return;
   {
     const int r = tid / kMfmaRows, b = tid % kMfmaRows;
     const int n = r0 + r;
@@ -769,6 +809,15 @@ int launch_mfma(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, 
   const int s1 = (h + 31) / 32, s2 = (inter + 31) / 32;
   const int n1 = (inter + kPairRows - 1) / kPairRows, n2 = (h + kPairRows - 1) / kPairRows;
   constexpr int kPackWaves = kPackThreads / kWave;
+  // Pairs run as full units except the last ones, cut into tiles: enough of
+  // them that the units left over after the last full round of resident
+  // workgroups (2 per CU) run at half size.
+  const int slots = 2 * cu_count();
+  auto full_pairs = [&](int pairs, int nsplit) {
+    const int rem = (pairs * nsplit) % slots;
+    return pairs - (rem + nsplit - 1) / nsplit;
+  };
+  const int f1 = full_pairs(n1, kSplit1), f2 = full_pairs(n2, kSplit2);
   for (int b0 = 0; b0 < batch; b0 += kMfmaRows) {
     const int nb = batch - b0 < kMfmaRows ? batch - b0 : kMfmaRows;
     const T* xb = x + size_t(b0) * h;
@@ -779,12 +828,12 @@ int launch_mfma(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, 
     // keep their x fragments in registers.
     auto* k1 = (s1 + 2 * kSplit1 - 1) / (2 * kSplit1) <= kXr ? ffn_gateup_mfma_kernel<T, kXr>
                                                               : ffn_gateup_mfma_kernel<T, 0>;
-    k1<<<kSplit1 * n1, kThreads, 0, stream>>>(wg, wu, ws.xf, ws.af, ws.p1, ws.cnt1, nb, h, inter);
+    k1<<<kSplit1 * (2 * n1 - f1), kThreads, 0, stream>>>(wg, wu, ws.xf, ws.af, ws.p1, ws.cnt1, nb, h, inter, f1);
     MKQ_LAUNCH_CHECK("ffn_gateup_mfma_kernel");
     auto* k2 = (s2 + kWaves * kSplit2 - 1) / (kWaves * kSplit2) <= kXr ? ffn_down_mfma_kernel<T, kXr>
                                                                        : ffn_down_mfma_kernel<T, 0>;
-    k2<<<kSplit2 * n2, kThreads, 0, stream>>>(wd, ws.af, xb, out + size_t(b0) * h, ws.p2, ws.cnt2, nb, h, inter,
-                                              add_residual);
+    k2<<<kSplit2 * (2 * n2 - f2), kThreads, 0, stream>>>(wd, ws.af, xb, out + size_t(b0) * h, ws.p2, ws.cnt2, nb, h,
+                                                         inter, add_residual, f2);
     MKQ_LAUNCH_CHECK("ffn_down_mfma_kernel");
   }
   return MKQ_OK;
