@@ -854,10 +854,32 @@ int launch_nb(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, T*
   const int max_lds = max_lds_per_block();
   const int hp = round_up(h, EPC), ip = round_up(inter, EPC);
 
-  // Both kernels: two workgroups per CU, rows split evenly -- except a down
-  // kernel whose act copy (NB rows, FP32) fills more than half of the LDS:
-  // one workgroup of 8 waves per CU.
-  const int rows1 = (inter + 2 * ncu - 1) / (2 * ncu);
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (int rc = set_lds_limit(&ffn_gateup_kernel<T, NB, VEC, CPL1>)) return rc;
+    if (int rc = set_lds_limit(&ffn_down_kernel<T, NB, VEC, CPL2, kThreads>)) return rc;
+    if (int rc = set_lds_limit(&ffn_down_kernel<T, NB, VEC, CPL2, 2 * kThreads>)) return rc;
+    attr_set = true;
+  }
+  // Gate/up: as many workgroups per CU as its registers and LDS let stay
+  // resident (at most 4), rows split evenly; more resident waves keep more
+  // rows in flight.  Down: two workgroups per CU -- except when the act copy
+  // (NB rows, FP32) fills more than half of the LDS: one workgroup of 8
+  // waves per CU.
+  const size_t lds1_max = sizeof(float) * (size_t(NB) * hp + kWaves * NB + size_t(2) * ((inter + ncu - 1) / ncu) * NB);
+  static size_t occ_lds = 0;
+  static int occ_wgs = 2;
+  if (occ_lds != lds1_max) {
+    int n = 0;
+    if (lds1_max > size_t(max_lds) ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, ffn_gateup_kernel<T, NB, VEC, CPL1>, kThreads, lds1_max) !=
+            hipSuccess ||
+        n < 1)
+      n = 2;
+    occ_wgs = n < 4 ? n : 4;
+    occ_lds = lds1_max;
+  }
+  const int rows1 = (inter + occ_wgs * ncu - 1) / (occ_wgs * ncu);
   const int grid1 = (inter + rows1 - 1) / rows1;
   const bool wide2 = 2 * sizeof(float) * (size_t(NB) * ip + size_t(h + 2 * ncu - 1) / (2 * ncu) * kQuarters * NB) >
                      size_t(max_lds);
@@ -869,13 +891,6 @@ int launch_nb(const T* x, const T* nw, const T* wg, const T* wu, const T* wd, T*
   if (lds1 > size_t(max_lds) || lds2 > size_t(max_lds))
     return set_error(MKQ_ERR_UNSUPPORTED, "dense_ffn_decode: hidden=%d / intermediate=%d too large for LDS staging", h,
                      inter);
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (int rc = set_lds_limit(&ffn_gateup_kernel<T, NB, VEC, CPL1>)) return rc;
-    if (int rc = set_lds_limit(&ffn_down_kernel<T, NB, VEC, CPL2, kThreads>)) return rc;
-    if (int rc = set_lds_limit(&ffn_down_kernel<T, NB, VEC, CPL2, 2 * kThreads>)) return rc;
-    attr_set = true;
-  }
   ffn_gateup_kernel<T, NB, VEC, CPL1><<<grid1, kThreads, lds1, stream>>>(x, nw, wg, wu, act, h, inter, eps, inter,
                                                                         rows1);
   MKQ_LAUNCH_CHECK("ffn_gateup_kernel");
