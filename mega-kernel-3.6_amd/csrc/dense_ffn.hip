@@ -371,8 +371,8 @@ constexpr int kLdsRow = 512 + 16;    // LDS stride of a staged row segment (byte
 constexpr int kWaveLds = kPairRows * kLdsRow;  // staged bytes per wave
 constexpr int kMaxPairs1 = 4096;     // intermediate <= 131072
 constexpr int kMaxPairs2 = 2048;     // hidden <= 65536
-constexpr int kPackThreads = 1024;   // K0: one k-step per wave
-constexpr int kPackUnroll = 8;       // K0: x chunks in flight per thread
+constexpr int kPackThreads = 512;    // K0: one k-step per wave
+constexpr int kPackUnroll = 10;      // K0: x chunks in flight per thread (8 rows x 5120 in one round)
 constexpr uint32_t kFarOff = 0x80000000u;
 constexpr int kXr = 20;              // k-steps per wave with register-resident x fragments (80 VGPRs)
 
@@ -441,8 +441,8 @@ inline MfmaWs mfma_ws(void* base, int h, int inter) {
   return w;
 }
 
-// K0: grid = ceil(s1 / 16), block 1024; wave w writes the fragment of k-step
-// 16 * blockIdx.x + w.  Every workgroup computes the rows' inverse RMS itself
+// K0: grid = ceil(s1 / 8), block 512; wave w writes the fragment of k-step
+// 8 * blockIdx.x + w.  Every workgroup computes the rows' inverse RMS itself
 // (x is a few KB, read from L2 with all loads of a thread in flight at once).
 template <typename T>
 __global__ __launch_bounds__(kPackThreads) void ffn_pack_x_kernel(const T* __restrict__ x, const T* __restrict__ nw,
